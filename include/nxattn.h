@@ -1,0 +1,130 @@
+/*
+ * nxattn -- fused scaled-dot-product attention (additive bias, boolean
+ * keep-mask, causal) for AMD Instinct MI355X (gfx950), C ABI.
+ *
+ * Drop-in boundary for nitrix's fused attention path.  The reference binds
+ * its fused kernel at
+ *   src/nitrix/nn/attention/__init__.py:63-123   (_attention_pallas, the
+ *                                                 dispatcher's call site)
+ *   src/nitrix/_kernels/cuda/attention.py:768-824 (scaled_dot_product_attention_pallas)
+ * and the entry points below replace, one for one, the pieces behind it:
+ *
+ *   nxa_check            <- _check_tileable           attention.py:708-765
+ *   nxa_fwd              <- _fused_forward_with_lse   attention.py:547-584
+ *                           + _mha_forward / nitrix_mha_forward
+ *                                                     attention.py:159-264, 85-156
+ *   nxa_bwd              <- _fused_backward           attention.py:600-653
+ *                           + _mha_backward / nitrix_mha_backward_kv, _q
+ *                                                     attention.py:390-499, 272-387
+ *                           + _unbroadcast (dbias)    attention.py:517-544
+ *   nxa_workspace_bytes  <- (XLA temp buffers of the broadcast_to / transpose
+ *                           glue at attention.py:560-569, 616-633; here a
+ *                           small caller-owned workspace instead)
+ *
+ * Conventions
+ *   - Every tensor is [B, H, L, D] (leading batch axes pre-flattened into B)
+ *     with unit stride over D.  Strides are in elements; the D stride is not
+ *     passed.  dO / dQ / dK / dV share the strides of O / Q / K / V.
+ *   - bias and mask are [B, H, Lq, Lk] with unit stride over Lk; a zero
+ *     stride broadcasts that axis (the reference's right-aligned
+ *     broadcast_to, without materialising it).  mask is one byte per entry,
+ *     nonzero = keep.  causal keeps key j for query i iff j <= i (indices
+ *     aligned at 0, also when Lq != Lk).
+ *   - lse is fp32 [B, H, Lq], natural log of sum_j exp(logit_ij).  A fully
+ *     masked query row yields O = NaN and lse = -inf, as the reference's
+ *     softmax over all -inf logits does.
+ *   - The library never allocates or frees device memory and never
+ *     synchronises the stream; the caller owns every buffer.  All work is
+ *     enqueued on `stream` (a hipStream_t, or NULL for the default stream).
+ *   - Return value 0 on success, a negative NXA_E_* code otherwise; the
+ *     message of the last failure on the calling thread is nxa_last_error().
+ */
+#ifndef NXATTN_H
+#define NXATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NXA_VERSION 1
+
+typedef enum { NXA_BF16 = 0, NXA_F32 = 1 } nxa_dtype;
+
+enum {
+  NXA_OK = 0,
+  NXA_E_ARG = -1,         /* null descriptor / pointer, bad enum value       */
+  NXA_E_SHAPE = -2,       /* non-positive or unsupported extents             */
+  NXA_E_DTYPE = -3,       /* dtype outside nxa_dtype                         */
+  NXA_E_LAYOUT = -4,      /* misaligned pointer or stride                    */
+  NXA_E_WORKSPACE = -5,   /* workspace smaller than nxa_workspace_bytes      */
+  NXA_E_LAUNCH = -6,      /* the HIP runtime rejected a kernel launch        */
+  NXA_E_UNSUPPORTED = -7  /* valid request this build does not tile          */
+};
+
+typedef struct {
+  int32_t B, H, Lq, Lk, D;  /* D <= 128, D % 8 == 0 (bf16) or % 4 (fp32)    */
+  int32_t io_dtype;         /* nxa_dtype of q, k, v, o, dO, dq, dk, dv       */
+  int32_t bias_dtype;       /* nxa_dtype of bias and dbias                   */
+  int32_t causal;           /* nonzero: keep key j for query i iff j <= i    */
+  float scale;              /* softmax scale applied to q.k                  */
+  int64_t q_str[3];         /* B, H, Lq strides of q (and dq)                */
+  int64_t k_str[3];         /* B, H, Lk strides of k (and dk)                */
+  int64_t v_str[3];         /* B, H, Lk strides of v (and dv)                */
+  int64_t o_str[3];         /* B, H, Lq strides of o (and dO)                */
+  int64_t bias_str[3];      /* B, H, Lq strides of bias; 0 = broadcast       */
+  int64_t mask_str[3];      /* B, H, Lq strides of mask; 0 = broadcast       */
+} nxa_desc;
+
+/* Library version (NXA_VERSION of the build). */
+int nxa_version(void);
+
+/* Host-only validation of a descriptor (no GPU needed).  `has_bias` and
+ * `has_mask` say whether the bias / mask strides are meaningful.
+ * Replaces _check_tileable (attention.py:708-765). */
+int nxa_check(const nxa_desc* desc, int has_bias, int has_mask);
+
+/* Bytes of caller-provided device workspace that nxa_fwd (is_bwd = 0) or
+ * nxa_bwd (is_bwd = 1) needs for this descriptor. */
+size_t nxa_workspace_bytes(const nxa_desc* desc, int has_bias, int has_mask,
+                           int is_bwd);
+
+/* Forward: o = softmax(scale * q k^T + bias, masked) v and its lse.
+ * bias / mask may be NULL; lse may be NULL.  When mask is given, the first
+ * nxa_workspace_bytes(desc, .., 0) bytes of the workspace receive the
+ * tile map that nxa_bwd can reuse (tilemap_ready = 1). */
+int nxa_fwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
+            const void* bias, const uint8_t* mask, void* o, float* lse,
+            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward: dq, dk, dv (and dbias if non-NULL) of sum(dO * o).
+ * dbias has the extent of bias (size 1 on the axes whose bias stride is 0)
+ * with strides dbias_str (B, H, Lq; unit stride over Lk); broadcast axes are
+ * summed, as the reference's _unbroadcast does.  `workspace` must hold
+ * nxa_workspace_bytes(desc, .., 1) bytes; when tilemap_ready is nonzero its
+ * leading bytes hold the tile map written by nxa_fwd for the same mask. */
+int nxa_bwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
+            const void* bias, const uint8_t* mask, const void* o,
+            const float* lse, const void* dout, void* dq, void* dk, void* dv,
+            void* dbias, const int64_t* dbias_str, void* workspace,
+            size_t workspace_bytes, int tilemap_ready, void* stream);
+
+/* Message of the last failure on this thread ("" if none). */
+const char* nxa_last_error(void);
+
+/* Kernel timing for profiling harnesses.  While enabled, every kernel the
+ * library launches is bracketed by HIP events on its stream; nxa_profile_read
+ * waits for them and returns the summed milliseconds and launch count of the
+ * kernels whose name starts with `kernel` ("fwd", "dkdv", "dq", "delta",
+ * "tilemap", "dbias_reduce").  Not for concurrent use from several threads. */
+int nxa_profile_enable(int on);
+int nxa_profile_read(const char* kernel, double* total_ms, int64_t* launches);
+int nxa_profile_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NXATTN_H */

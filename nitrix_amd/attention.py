@@ -1,0 +1,519 @@
+"""Scaled-dot-product attention with a fused gfx950 engine.
+
+Host side of the drop-in for nitrix's attention path.  It keeps the
+reference's public call signature and layering:
+
+* :func:`scaled_dot_product_attention` -- the public dispatcher
+  (``src/nitrix/nn/attention/__init__.py:126-230``): validation, default
+  scale, backend resolution, qk-norm outside the fused core, loud fallback.
+* :func:`scaled_dot_product_attention_hip` -- the fused entry point, the
+  counterpart of ``scaled_dot_product_attention_pallas``
+  (``src/nitrix/_kernels/cuda/attention.py:768-824``): a tileability gate
+  (:func:`_check_tileable`, ``:708-765``) and a differentiable wrapper
+  (:class:`_SdpaHip`, the ``custom_vjp`` of ``:661-700``) around the C ABI of
+  ``libnxattn.so``.
+* :func:`reference_scaled_dot_product_attention` -- the unfused reference
+  engine (``backend='jax'``), the recipe of
+  ``src/nitrix/nn/attention/_reference.py:80-181`` in stock tensor ops.
+
+Tensors live on the device (PyTorch-ROCm provides memory and streams); the
+fused path launches on the current stream of the tensors' device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._backend import (
+    NitrixBackendError,
+    fallback,
+    resolve_backend,
+)
+
+__all__ = [
+    'HipNotTileable',
+    'default_scale',
+    'qk_rms_norm',
+    'reference_scaled_dot_product_attention',
+    'scaled_dot_product_attention',
+    'scaled_dot_product_attention_hip',
+]
+
+# RMS-norm epsilon for qk-norm (_reference.py:32).
+_QK_RMS_EPS = 1e-6
+
+_IO_DTYPES = {torch.bfloat16: _lib.NXA_BF16, torch.float32: _lib.NXA_F32}
+_MAX_HEAD_DIM = 128
+
+
+class HipNotTileable(RuntimeError):
+    """The fused kernel declines this shape / dtype (the counterpart of the
+    reference's ``PallasNotTileable``, ``attention.py:71-77``); the dispatcher
+    turns it into a loud fallback to the reference engine."""
+
+
+def default_scale(head_dim: int) -> float:
+    """``1 / sqrt(d)`` (``_reference.py:35-49``)."""
+    return 1.0 / math.sqrt(float(head_dim))
+
+
+def qk_rms_norm(z: torch.Tensor) -> torch.Tensor:
+    """``z * rsqrt(mean(z^2, -1) + 1e-6)`` (``_reference.py:52-77``).
+
+    Computed in at least float32 and returned in ``z``'s dtype.
+    """
+    acc = torch.promote_types(z.dtype, torch.float32)
+    zf = z.to(acc)
+    ms = zf.square().mean(dim=-1, keepdim=True)
+    return (zf * torch.rsqrt(ms + _QK_RMS_EPS)).to(z.dtype)
+
+
+def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    """``__init__.py:40-60``: same checks, same exception type."""
+    if q.ndim < 3 or k.ndim < 3 or v.ndim < 3:
+        raise ValueError(
+            'scaled_dot_product_attention: q, k, v must have at least 3 '
+            'dims (..., h, s, d); got ndim '
+            f'{q.ndim}, {k.ndim}, {v.ndim}.'
+        )
+    if q.shape[-1] != k.shape[-1]:
+        raise ValueError(
+            'scaled_dot_product_attention: q/k head-dim mismatch '
+            f'(q d={q.shape[-1]}, k d={k.shape[-1]}).'
+        )
+    if k.shape[-2] != v.shape[-2]:
+        raise ValueError(
+            'scaled_dot_product_attention: k/v key-length mismatch '
+            f'(k t={k.shape[-2]}, v t={v.shape[-2]}).'
+        )
+
+
+# ---------------------------------------------------------------------------
+# Reference engine (backend='jax')
+# ---------------------------------------------------------------------------
+
+
+def reference_scaled_dot_product_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    bias: Optional[torch.Tensor] = None,
+    mask: Optional[torch.Tensor] = None,
+    scale: Optional[float] = None,
+    causal: bool = False,
+    qk_norm: bool = False,
+) -> torch.Tensor:
+    """Unfused attention, op for op as ``_reference.py:80-181``.
+
+    Upcast to ``promote(result_type(q, k, v), float32)``, optional qk-norm,
+    ``q k^T``, ``* scale``, ``+ bias``, ``where(mask & causal, ., -inf)``,
+    softmax, ``. v``, cast back.  A fully masked row yields NaN.
+    """
+    if scale is None:
+        scale = default_scale(q.shape[-1])
+    out_dtype = torch.promote_types(torch.promote_types(q.dtype, k.dtype), v.dtype)
+    acc = torch.promote_types(out_dtype, torch.float32)
+    q = q.to(acc)
+    k = k.to(acc)
+    v = v.to(acc)
+    if qk_norm:
+        q = qk_rms_norm(q)
+        k = qk_rms_norm(k)
+    logits = torch.matmul(q, k.transpose(-1, -2).contiguous()) * scale
+    if bias is not None:
+        logits = logits + bias.to(acc)
+    keep = mask
+    if causal:
+        s, t = logits.shape[-2], logits.shape[-1]
+        cm = (
+            torch.arange(s, device=logits.device)[:, None]
+            >= torch.arange(t, device=logits.device)[None, :]
+        )
+        keep = cm if keep is None else (keep.to(torch.bool) & cm)
+    if keep is not None:
+        logits = torch.where(
+            keep.to(torch.bool), logits, torch.full((), -math.inf, dtype=acc, device=logits.device)
+        )
+    weights = torch.softmax(logits, dim=-1)
+    out = torch.matmul(weights, v)
+    return out.to(out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# Fused HIP engine
+# ---------------------------------------------------------------------------
+
+
+def _check_tileable(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    """Reject shapes the gfx950 kernels cannot run (``attention.py:708-765``).
+
+    Accepts bf16 or fp32 (q, k, v of one dtype), ``d_v == d``, head dim up to
+    128 (a multiple of 8 for bf16, of 4 for fp32) and any positive query / key
+    lengths (tails are predicated in the kernels).
+    """
+    if q.dtype not in _IO_DTYPES:
+        raise HipNotTileable(
+            f'fused attention supports bfloat16 and float32; got {q.dtype}.'
+        )
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise HipNotTileable(
+            f'fused attention needs one dtype for q, k, v; got {q.dtype}, '
+            f'{k.dtype}, {v.dtype}.'
+        )
+    d, d_v = q.shape[-1], v.shape[-1]
+    if d_v != d:
+        raise HipNotTileable(
+            f'fused attention requires d_v == d; got d={d}, d_v={d_v}.'
+        )
+    epc = 8 if q.dtype == torch.bfloat16 else 4
+    if d > _MAX_HEAD_DIM or d % epc != 0:
+        raise HipNotTileable(
+            f'fused attention requires head dim <= {_MAX_HEAD_DIM} and a '
+            f'multiple of {epc}; got {d}.'
+        )
+    if q.shape[-2] == 0 or k.shape[-2] == 0 or d == 0:
+        raise HipNotTileable('fused attention needs non-empty q / k / v.')
+    if not (q.device == k.device == v.device):
+        raise HipNotTileable('q, k, v are on different devices.')
+
+
+def _layout_ok(x: torch.Tensor, epc: int) -> bool:
+    if x.stride(-1) != 1 and x.shape[-1] != 1:
+        return False
+    if x.data_ptr() % 16 != 0:
+        return False
+    return all(s % epc == 0 for s in x.stride()[:-1])
+
+
+def _as_bhld(x: torch.Tensor, lead: Sequence[int], nb: int, epc: int) -> torch.Tensor:
+    L, d = x.shape[-2], x.shape[-1]
+    h = lead[-1]
+    y = x.expand(*lead, L, d).reshape(nb, h, L, d)
+    if not _layout_ok(y, epc):
+        y = y.contiguous()
+    return y
+
+
+def _as_bhst(
+    x: torch.Tensor, lead: Sequence[int], nb: int, s: int, t: int
+) -> torch.Tensor:
+    h = lead[-1]
+    y = x.expand(*lead, s, t).reshape(nb, h, s, t)
+    if y.stride(-1) != 1 and t != 1:
+        y = y.contiguous()
+    return y
+
+
+def _unbroadcast(g: torch.Tensor, shape: Sequence[int]) -> torch.Tensor:
+    """VJP of a broadcast (``attention.py:517-544``)."""
+    while g.ndim > len(shape):
+        g = g.sum(dim=0)
+    axes = tuple(i for i, n in enumerate(shape) if n == 1 and g.shape[i] != 1)
+    if axes:
+        g = g.sum(dim=axes, keepdim=True)
+    return g.reshape(tuple(shape))
+
+
+def _ptr(x: Optional[torch.Tensor]) -> Optional[int]:
+    return None if x is None else x.data_ptr()
+
+
+class _Prepared:
+    """Flattened [nb, h, L, d] views plus the C descriptor of one call."""
+
+    def __init__(self, q, k, v, bias, mask, scale, causal):
+        *_, s, d = q.shape
+        t = k.shape[-2]
+        lead = tuple(torch.broadcast_shapes(q.shape[:-2], k.shape[:-2], v.shape[:-2]))
+        self.lead = lead
+        self.batch = lead[:-1]
+        self.h = lead[-1]
+        self.nb = int(math.prod(self.batch)) if self.batch else 1
+        self.s, self.t, self.d = s, t, d
+        self.dtype = q.dtype
+        self.device = q.device
+        self.epc = 8 if q.dtype == torch.bfloat16 else 4
+        self.q = _as_bhld(q, lead, self.nb, self.epc)
+        self.k = _as_bhld(k, lead, self.nb, self.epc)
+        self.v = _as_bhld(v, lead, self.nb, self.epc)
+        self.bias_shape = None if bias is None else tuple(bias.shape)
+        self.bias_dtype = None if bias is None else bias.dtype
+        self.bias = None
+        if bias is not None:
+            b = bias.to(self.device)
+            if b.dtype not in (torch.bfloat16, torch.float32):
+                b = b.to(torch.float32)
+            self.bias = _as_bhst(b, lead, self.nb, s, t)
+        self.mask = None
+        if mask is not None:
+            m = mask.to(self.device)
+            if m.dtype not in (torch.bool, torch.uint8):
+                m = m != 0
+            self.mask = _as_bhst(m, lead, self.nb, s, t)
+
+        desc = _lib.NxaDesc()
+        desc.B, desc.H, desc.Lq, desc.Lk, desc.D = self.nb, self.h, s, t, d
+        desc.io_dtype = _IO_DTYPES[q.dtype]
+        desc.bias_dtype = (
+            _lib.NXA_BF16
+            if self.bias is not None and self.bias.dtype == torch.bfloat16
+            else _lib.NXA_F32
+        )
+        desc.causal = 1 if causal else 0
+        desc.scale = float(scale)
+        desc.q_str[:] = self.q.stride()[:3]
+        desc.k_str[:] = self.k.stride()[:3]
+        desc.v_str[:] = self.v.stride()[:3]
+        # outputs are allocated contiguous
+        desc.o_str[:] = (self.h * s * d, s * d, d)
+        if self.bias is not None:
+            desc.bias_str[:] = self.bias.stride()[:3]
+        if self.mask is not None:
+            desc.mask_str[:] = self.mask.stride()[:3]
+        self.desc = desc
+
+    @property
+    def has_bias(self) -> int:
+        return 1 if self.bias is not None else 0
+
+    @property
+    def has_mask(self) -> int:
+        return 1 if self.mask is not None else 0
+
+    def stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def workspace(self, is_bwd: int) -> Optional[torch.Tensor]:
+        nbytes = _lib.lib().nxa_workspace_bytes(
+            ctypes.byref(self.desc), self.has_bias, self.has_mask, is_bwd
+        )
+        if nbytes == 0:
+            return None
+        return torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+
+
+def _forward(prep: _Prepared):
+    """Run ``nxa_fwd``; returns ``(o [nb,h,s,d], lse [nb,h,s], workspace)``."""
+    lib = _lib.lib()
+    o = torch.empty(
+        (prep.nb, prep.h, prep.s, prep.d), dtype=prep.dtype, device=prep.device
+    )
+    lse = torch.empty(
+        (prep.nb, prep.h, prep.s), dtype=torch.float32, device=prep.device
+    )
+    ws = prep.workspace(0)
+    _lib.check(
+        lib.nxa_fwd(
+            ctypes.byref(prep.desc),
+            _ptr(prep.q),
+            _ptr(prep.k),
+            _ptr(prep.v),
+            _ptr(prep.bias),
+            _ptr(prep.mask),
+            _ptr(o),
+            _ptr(lse),
+            _ptr(ws),
+            0 if ws is None else ws.numel(),
+            prep.stream(),
+        )
+    )
+    return o, lse, ws
+
+
+def _dbias_geometry(prep: _Prepared):
+    bs = prep.desc.bias_str
+    ob = 1 if bs[0] == 0 else prep.nb
+    oh = 1 if bs[1] == 0 else prep.h
+    lq = 1 if (prep.s > 1 and bs[2] == 0) else prep.s
+    return ob, oh, lq
+
+
+def _backward(prep: _Prepared, o, lse, fwd_ws, dout, want_dbias: bool):
+    """Run ``nxa_bwd``; returns flattened ``(dq, dk, dv, dbias_kernel)``."""
+    lib = _lib.lib()
+    # dK / dV are written per (b, h): broadcast q / k / v are materialised.
+    q = prep.q if all(x != 0 for x in prep.q.stride()[:2]) else prep.q.contiguous()
+    k = prep.k if all(x != 0 for x in prep.k.stride()[:2]) else prep.k.contiguous()
+    v = prep.v if all(x != 0 for x in prep.v.stride()[:2]) else prep.v.contiguous()
+    if q is not prep.q or k is not prep.k or v is not prep.v:
+        prep.desc.q_str[:] = q.stride()[:3]
+        prep.desc.k_str[:] = k.stride()[:3]
+        prep.desc.v_str[:] = v.stride()[:3]
+    dout = dout.reshape(prep.nb, prep.h, prep.s, prep.d)
+    if not dout.is_contiguous() or dout.data_ptr() % 16 != 0:
+        dout = dout.contiguous()
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    if dq.stride() != q.stride() or dk.stride() != k.stride() or dv.stride() != v.stride():
+        # gradients share the input strides in the C ABI
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        prep.desc.q_str[:] = q.stride()[:3]
+        prep.desc.k_str[:] = k.stride()[:3]
+        prep.desc.v_str[:] = v.stride()[:3]
+    dbias = None
+    dbias_str = None
+    if want_dbias and prep.bias is not None:
+        ob, oh, lq = _dbias_geometry(prep)
+        dbias = torch.empty(
+            (ob, oh, lq, prep.t), dtype=prep.bias.dtype, device=prep.device
+        )
+        dbias_str = (ctypes.c_int64 * 3)(oh * lq * prep.t, lq * prep.t, prep.t)
+    ws = prep.workspace(1)
+    ready = 0
+    if prep.mask is not None and fwd_ws is not None:
+        n_tm = fwd_ws.numel()
+        ws[:n_tm].copy_(fwd_ws)
+        ready = 1
+    _lib.check(
+        lib.nxa_bwd(
+            ctypes.byref(prep.desc),
+            _ptr(q),
+            _ptr(k),
+            _ptr(v),
+            _ptr(prep.bias),
+            _ptr(prep.mask),
+            _ptr(o),
+            _ptr(lse),
+            _ptr(dout),
+            _ptr(dq),
+            _ptr(dk),
+            _ptr(dv),
+            _ptr(dbias),
+            dbias_str,
+            _ptr(ws),
+            ws.numel(),
+            ready,
+            prep.stream(),
+        )
+    )
+    return dq, dk, dv, dbias
+
+
+class _SdpaHip(torch.autograd.Function):
+    """Differentiable fused attention: ``(q, k, v, bias, mask) -> out``.
+
+    ``scale`` and ``causal`` are non-differentiable; the mask gets no
+    gradient -- the structure of the reference's ``custom_vjp``
+    (``attention.py:661-700``)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bias, mask, scale, causal):
+        prep = _Prepared(q, k, v, bias, mask, scale, causal)
+        o, lse, ws = _forward(prep)
+        ctx.prep = prep
+        ctx.shapes = (tuple(q.shape), tuple(k.shape), tuple(v.shape))
+        ctx.save_for_backward(o, lse, ws if ws is not None else torch.empty(0))
+        return o.reshape(*prep.lead, prep.s, prep.d)
+
+    @staticmethod
+    def backward(ctx, dout):
+        o, lse, ws = ctx.saved_tensors
+        prep: _Prepared = ctx.prep
+        want_dbias = bool(ctx.needs_input_grad[3])
+        dq, dk, dv, dbias_k = _backward(
+            prep, o, lse, ws if ws.numel() else None, dout, want_dbias
+        )
+        qs, ks, vs = ctx.shapes
+        lead = prep.lead
+        dq = _unbroadcast(dq.reshape(*lead, prep.s, prep.d), qs)
+        dk = _unbroadcast(dk.reshape(*lead, prep.t, prep.d), ks)
+        dv = _unbroadcast(dv.reshape(*lead, prep.t, prep.d), vs)
+        dbias = None
+        if dbias_k is not None:
+            ob, oh, lq = dbias_k.shape[:3]
+            bdims = list(prep.batch) if ob > 1 else [1] * len(prep.batch)
+            g = dbias_k.reshape(*bdims, oh, lq, prep.t)
+            dbias = _unbroadcast(g, prep.bias_shape).to(prep.bias_dtype)
+        return dq, dk, dv, dbias, None, None, None
+
+
+def scaled_dot_product_attention_hip(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    scale: float,
+    bias: Optional[torch.Tensor] = None,
+    mask: Optional[torch.Tensor] = None,
+    causal: bool = False,
+) -> torch.Tensor:
+    """Fused attention on gfx950 (``attention.py:768-824`` counterpart).
+
+    Raises :class:`HipNotTileable` for shapes outside the supported set; the
+    dispatcher turns that into a loud fallback.  Differentiable in q, k, v and
+    bias.
+    """
+    _check_tileable(q, k, v)
+    _lib.lib()  # a missing library is an error here, not a fallback
+    return _SdpaHip.apply(q, k, v, bias, mask, float(scale), bool(causal))
+
+
+def scaled_dot_product_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    bias: Optional[torch.Tensor] = None,
+    mask: Optional[torch.Tensor] = None,
+    scale: Optional[float] = None,
+    causal: bool = False,
+    qk_norm: bool = False,
+    backend: str = 'auto',
+) -> torch.Tensor:
+    """Scaled-dot-product attention with backend dispatch
+    (``src/nitrix/nn/attention/__init__.py:126-230``).
+
+    ``softmax(scale * q k^T + bias [masked]) v`` over the key axis.  q/k/v are
+    ``(..., h, s, d)`` / ``(..., h, t, d)`` / ``(..., h, t, d_v)``; bias and the
+    boolean keep-mask broadcast to ``(..., h, s, t)``; ``causal`` keeps key
+    ``j`` for query ``i`` iff ``j <= i``; ``scale`` defaults to ``1/sqrt(d)``;
+    ``qk_norm`` RMS-normalises q and k over the head dim first.
+
+    ``backend``: ``'hip'`` (fused gfx950 kernels), ``'jax'`` (the unfused
+    reference engine) or ``'auto'`` (``'hip'`` on a gfx950 device, else
+    ``'jax'``; ``NITRIX_BACKEND`` and reproducible mode as in the reference).
+    """
+    _validate(q, k, v)
+    resolved_scale = default_scale(q.shape[-1]) if scale is None else scale
+    resolved = resolve_backend(backend, q.device)
+    if resolved == 'hip':
+        q_in = qk_rms_norm(q) if qk_norm else q
+        k_in = qk_rms_norm(k) if qk_norm else k
+        try:
+            return scaled_dot_product_attention_hip(
+                q_in,
+                k_in,
+                v,
+                bias=bias,
+                mask=mask,
+                scale=resolved_scale,
+                causal=causal,
+            )
+        except HipNotTileable as exc:
+            fallback(
+                function='scaled_dot_product_attention',
+                requested='hip',
+                resolved='jax',
+                reason=f'the fused attention kernel does not support this shape ({exc})',
+                shapes=(tuple(q.shape), tuple(k.shape), tuple(v.shape)),
+                dtype=q.dtype,
+            )
+        except _lib.HipLibraryMissing as exc:
+            raise NitrixBackendError(str(exc)) from exc
+    return reference_scaled_dot_product_attention(
+        q,
+        k,
+        v,
+        bias=bias,
+        mask=mask,
+        scale=resolved_scale,
+        causal=causal,
+        qk_norm=qk_norm,
+    )

@@ -1,0 +1,507 @@
+// Backward pass: delta = rowsum(O * dO), then two deterministic kernels
+// (no atomics): dK/dV (+ dbias) with a grid over key tiles, and dQ with a
+// grid over query tiles.  Both recompute P from the forward's LSE.
+//
+// Replaces the reference's backward glue and Pallas launches:
+// src/nitrix/_kernels/cuda/attention.py:600-653 (delta, broadcast,
+// unbroadcast), :390-499 (launches), :272-332 (dK/dV kernel), :335-387
+// (dQ kernel), :517-544 (unbroadcast of dbias; folded in here as an
+// in-kernel column sum or a reduction kernel).
+#include "nxa_common.h"
+#include "nxa_launch.h"
+
+namespace nxa {
+
+// ---------------------------------------------------------------------------
+// delta[b, h, q] = sum_d O[q, d] * dO[q, d]  (fp32).  16 lanes per row.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void delta_kernel(const Params p) {
+  using Frag = typename Mma<T>::Frag;
+  constexpr int EPC = Mma<T>::EPC;
+  const int rows = p.B * p.H * p.Lq;
+  const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  float acc = 0.f;
+  if (row < rows) {
+    const int q = row % p.Lq;
+    const int bh = row / p.Lq;
+    const int b = bh / p.H, h = bh % p.H;
+    const int64_t off = b * p.o_str[0] + h * p.o_str[1] + (int64_t)q * p.o_str[2];
+    const T* o = (const T*)p.o + off;
+    const T* d = (const T*)p.dout + off;
+    for (int c = sub * EPC; c < p.D; c += 16 * EPC) {
+      const Frag x = ld16(o + c), y = ld16(d + c);
+#pragma unroll
+      for (int j = 0; j < EPC; ++j) acc += to_f32(x[j]) * to_f32(y[j]);
+    }
+  }
+  acc += __shfl_xor(acc, 8, 16);
+  acc += __shfl_xor(acc, 4, 16);
+  acc += __shfl_xor(acc, 2, 16);
+  acc += __shfl_xor(acc, 1, 16);
+  if (row < rows && sub == 0) p.delta[row] = acc;
+}
+
+// Loads a [ROWS x DP] tile (rows r0.., unit-stride head dim) into a row-major
+// LDS tile `dst` (row stride SK) and, when TRANS, also into a transposed LDS
+// tile `dstT` (row stride STT, row index = head dim).
+template <typename T, int DP, int ROWS, int SK, int STT, bool TRANS>
+__device__ __forceinline__ void load_tile(const T* src, int64_t rs, int r0,
+                                          int nrows, int D, T* dst, T* dstT,
+                                          int tid) {
+  using Frag = typename Mma<T>::Frag;
+  constexpr int EPC = Mma<T>::EPC;
+  constexpr int CPR = DP / EPC;
+  if constexpr (sizeof(T) == 2 && TRANS) {
+    // Pairs of rows so that transposed writes are 32-bit.
+#pragma unroll
+    for (int i = tid; i < (ROWS / 2) * CPR; i += 256) {
+      const int rp = i / CPR, cc = i % CPR;
+      const int r = 2 * rp, d = cc * EPC;
+      Frag x0 = zero_frag<T>(), x1 = zero_frag<T>();
+      if (d < D) {
+        if (r0 + r < nrows) x0 = ld16(src + (int64_t)(r0 + r) * rs + d);
+        if (r0 + r + 1 < nrows) x1 = ld16(src + (int64_t)(r0 + r + 1) * rs + d);
+      }
+      *reinterpret_cast<Frag*>(&dst[r * SK + d]) = x0;
+      *reinterpret_cast<Frag*>(&dst[(r + 1) * SK + d]) = x1;
+#pragma unroll
+      for (int j = 0; j < EPC; ++j) {
+        bf16 pair[2] = {x0[j], x1[j]};
+        *reinterpret_cast<uint32_t*>(&dstT[(d + j) * STT + r]) =
+            *reinterpret_cast<uint32_t*>(pair);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = tid; i < ROWS * CPR; i += 256) {
+      const int r = i / CPR, cc = i % CPR;
+      const int d = cc * EPC;
+      Frag x = zero_frag<T>();
+      if (r0 + r < nrows && d < D) x = ld16(src + (int64_t)(r0 + r) * rs + d);
+      *reinterpret_cast<Frag*>(&dst[r * SK + d]) = x;
+      if constexpr (TRANS) {
+#pragma unroll
+        for (int j = 0; j < EPC; ++j) dstT[(d + j) * STT + r] = x[j];
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void store_dbias(const Params& p, int64_t off,
+                                            float x) {
+  if (p.dbias_f32 || p.bias_dtype == kF32)
+    reinterpret_cast<float*>(p.dbias)[off] = x;
+  else
+    reinterpret_cast<bf16*>(p.dbias)[off] = (bf16)x;
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV (and dbias).  Block = 4 waves x 32 keys; loops over 64-query tiles.
+// Each wave computes S = Q K^T and dP = dO V^T with the key as the lane's
+// column, so P and dS feed dV^T = dO^T P and dK^T = Q^T dS as reduction
+// operands straight from registers.
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
+  using M = Mma<T>;
+  using Frag = typename M::Frag;
+  constexpr int EPC = M::EPC, KC = M::KC;
+  constexpr int BNK = 128, BQ = 64;
+  constexpr int SK = DP + EPC;
+  constexpr int ST = BQ + 4;
+  constexpr int NC = DP / KC;
+  constexpr int NDB = DP / 32;
+  constexpr int FPB = M::FRAGS_PER_BLOCK;
+  __shared__ __attribute__((aligned(16))) T Qs[BQ * SK];
+  __shared__ __attribute__((aligned(16))) T Qt[DP * ST];
+  __shared__ __attribute__((aligned(16))) T Ds[BQ * SK];
+  __shared__ __attribute__((aligned(16))) T Dt[DP * ST];
+  __shared__ float lse_s[BQ], dlt_s[BQ];
+
+  const int nblk = p.B * p.H * p.nkt;
+  const int vid = xcd_remap(blockIdx.x, nblk);
+  const int bh = vid / p.nkt;
+  const int kt = vid % p.nkt;
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, c32 = lane & 31;
+  const int kblk0 = kt * BNK;
+  const int kw0 = kblk0 + wave * 32;
+  const int key = kw0 + c32;
+  const bool kok = key < p.Lk;
+  const int kclamp = kok ? key : p.Lk - 1;
+
+  const T* qp = (const T*)p.q + b * p.q_str[0] + h * p.q_str[1];
+  const T* kp = (const T*)p.k + b * p.k_str[0] + h * p.k_str[1];
+  const T* vp = (const T*)p.v + b * p.v_str[0] + h * p.v_str[1];
+  const T* dop = (const T*)p.dout + b * p.o_str[0] + h * p.o_str[1];
+  const float* lsep = p.lse + ((int64_t)b * p.H + h) * p.Lq;
+  const float* dltp = p.delta + ((int64_t)b * p.H + h) * p.Lq;
+
+  Frag kf[NC], vf[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int d = c * KC + g * EPC;
+    const bool ok = kok && d < p.D;
+    kf[c] = ok ? ld16(kp + (int64_t)key * p.k_str[2] + d) : zero_frag<T>();
+    vf[c] = ok ? ld16(vp + (int64_t)key * p.v_str[2] + d) : zero_frag<T>();
+  }
+  f32x16 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dk[db][r] = 0.f;
+      dv[db][r] = 0.f;
+    }
+  float colsum = 0.f;
+
+  const int64_t bbase =
+      p.has_bias ? b * p.bias_str[0] + h * p.bias_str[1] + kclamp : 0;
+  const uint8_t* mbase =
+      p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] + kclamp
+                 : nullptr;
+  const int64_t dbbase = b * p.dbias_str[0] + h * p.dbias_str[1] + key;
+  const bool full_db = p.dbias_mode == kDbiasFull;
+
+  const int nq = (p.Lq + BQ - 1) / BQ;
+  for (int qt = 0; qt < nq; ++qt) {
+    const int q0 = qt * BQ;
+    bool active = !p.causal || (q0 + BQ - 1 >= kblk0);
+    int cls = 3;
+    if (active && p.has_tilemap)
+      cls = tile_class(p, b, h, q0, q0 + BQ, kblk0, kblk0 + BNK);
+    active = active && (cls & 1);
+    if (!active) {
+      if (full_db && kok) {
+        for (int i = 0; i < BQ; ++i)
+          if (q0 + i < p.Lq) store_dbias(p, dbbase + (int64_t)(q0 + i) * p.dbias_str[2], 0.f);
+      }
+      continue;
+    }
+    __syncthreads();
+    load_tile<T, DP, BQ, SK, ST, true>(qp, p.q_str[2], q0, p.Lq, p.D, Qs, Qt, tid);
+    load_tile<T, DP, BQ, SK, ST, true>(dop, p.o_str[2], q0, p.Lq, p.D, Ds, Dt, tid);
+    if (tid < BQ) {
+      const int q = q0 + tid;
+      lse_s[tid] = q < p.Lq ? lsep[q] * kLog2e : 0.f;
+      dlt_s[tid] = q < p.Lq ? dltp[q] : 0.f;
+    }
+    __syncthreads();
+
+    f32x16 s[2], dp[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[qb][r] = 0.f;
+        dp[qb][r] = 0.f;
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int off = (qb * 32 + c32) * SK + c * KC + g * EPC;
+        M::run(s[qb], ld16(&Qs[off]), kf[c]);
+        M::run(dp[qb], ld16(&Ds[off]), vf[c]);
+      }
+    }
+
+    const bool need_mask = p.has_mask && !(cls & 2);
+    const bool diag = p.causal && (kw0 + 31 > q0);
+    const bool tail = (q0 + BQ > p.Lq) || (kw0 + 32 > p.Lk);
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int ql = qb * 32 + 8 * (r / 4) + 4 * g + (r % 4);
+        const int q = q0 + ql;
+        const int qc = q < p.Lq ? q : p.Lq - 1;
+        float x = s[qb][r] * p.scale_log2;
+        if (p.has_bias) {
+          const int64_t off = bbase + (int64_t)qc * p.bias_str[2];
+          const float bv = p.bias_dtype == kBF16
+                               ? (float)reinterpret_cast<const bf16*>(p.bias)[off]
+                               : reinterpret_cast<const float*>(p.bias)[off];
+          x = __builtin_fmaf(bv, kLog2e, x);
+        }
+        bool keep = true;
+        if (need_mask) keep = mbase[(int64_t)qc * p.mask_str[2]] != 0;
+        if (tail) keep = keep && q < p.Lq && kok;
+        if (diag) keep = keep && key <= q;
+        const float pr = keep ? fast_exp2(x - lse_s[ql]) : 0.f;
+        const float ds = pr * (dp[qb][r] - dlt_s[ql]);
+        s[qb][r] = pr;
+        dp[qb][r] = ds;
+        if (full_db && kok && q < p.Lq)
+          store_dbias(p, dbbase + (int64_t)q * p.dbias_str[2], ds);
+        colsum += ds;
+      }
+
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const T* rowd = &Dt[(db * 32 + c32) * ST];
+      const T* rowq = &Qt[(db * 32 + c32) * ST];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int f = 0; f < FPB; ++f) {
+          M::run(dv[db], lds_frag_t<T>(rowd + qb * 32, g, f), M::pack(s[qb], f));
+          M::run(dk[db], lds_frag_t<T>(rowq + qb * 32, g, f), M::pack(dp[qb], f));
+        }
+    }
+  }
+
+  if (kok) {
+    T* dkp = (T*)p.dk + b * p.k_str[0] + h * p.k_str[1] + (int64_t)key * p.k_str[2];
+    T* dvp = (T*)p.dv + b * p.v_str[0] + h * p.v_str[1] + (int64_t)key * p.v_str[2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d0 = db * 32 + 8 * c + 4 * g;
+        if (d0 < p.D) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            dkp[d0 + j] = from_f32<T>(dk[db][4 * c + j] * p.scale);
+            dvp[d0 + j] = from_f32<T>(dv[db][4 * c + j]);
+          }
+        }
+      }
+  }
+  if (p.dbias_mode == kDbiasColsum) {
+    const float tot = colsum + shfl_xor32(colsum);
+    if (kok && g == 0) store_dbias(p, dbbase, tot);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ.  Block = 4 waves x 32 queries; loops over 64-key tiles.  Each wave
+// computes S^T = K Q^T and dP^T = V dO^T (query = lane column) so dS^T feeds
+// dQ^T = K^T dS^T from registers.
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void dq_kernel(const Params p) {
+  using M = Mma<T>;
+  using Frag = typename M::Frag;
+  constexpr int EPC = M::EPC, KC = M::KC;
+  constexpr int BM = 128, BN = 64;
+  constexpr int SK = DP + EPC;
+  constexpr int ST = BN + 4;
+  constexpr int NC = DP / KC;
+  constexpr int NDB = DP / 32;
+  constexpr int FPB = M::FRAGS_PER_BLOCK;
+  __shared__ __attribute__((aligned(16))) T Ks[BN * SK];
+  __shared__ __attribute__((aligned(16))) T Vs[BN * SK];
+  __shared__ __attribute__((aligned(16))) T Kt[DP * ST];
+
+  const int nblk = p.B * p.H * p.nqt;
+  const int vid = xcd_remap(blockIdx.x, nblk);
+  const int bh = vid / p.nqt;
+  const int qt = p.nqt - 1 - (vid % p.nqt);
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, c32 = lane & 31;
+  const int q0 = qt * BM;
+  const int qw0 = q0 + wave * 32;
+  const int qrow = qw0 + c32;
+  const bool qok = qrow < p.Lq;
+  const int qclamp = qok ? qrow : p.Lq - 1;
+
+  const T* qp = (const T*)p.q + b * p.q_str[0] + h * p.q_str[1];
+  const T* kp = (const T*)p.k + b * p.k_str[0] + h * p.k_str[1];
+  const T* vp = (const T*)p.v + b * p.v_str[0] + h * p.v_str[1];
+  const T* dop = (const T*)p.dout + b * p.o_str[0] + h * p.o_str[1];
+
+  Frag qf[NC], df[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int d = c * KC + g * EPC;
+    const bool ok = qok && d < p.D;
+    qf[c] = ok ? ld16(qp + (int64_t)qrow * p.q_str[2] + d) : zero_frag<T>();
+    df[c] = ok ? ld16(dop + (int64_t)qrow * p.o_str[2] + d) : zero_frag<T>();
+  }
+  const int64_t rowid = ((int64_t)b * p.H + h) * p.Lq + qclamp;
+  const float lse2 = p.lse[rowid] * kLog2e;
+  const float dlt = p.delta[rowid];
+
+  f32x16 dq[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
+
+  int k_end = p.Lk;
+  if (p.causal) k_end = min(k_end, q0 + BM);
+  const int nkt = (k_end + BN - 1) / BN;
+  const int64_t brow =
+      p.has_bias ? b * p.bias_str[0] + h * p.bias_str[1] +
+                       (int64_t)qclamp * p.bias_str[2]
+                 : 0;
+  const uint8_t* mrow =
+      p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] +
+                       (int64_t)qclamp * p.mask_str[2]
+                 : nullptr;
+
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int k0 = kt * BN;
+    int cls = 3;
+    if (p.has_tilemap) cls = tile_class(p, b, h, q0, q0 + BM, k0, k0 + BN);
+    if (!(cls & 1)) continue;
+    __syncthreads();
+    load_tile<T, DP, BN, SK, ST, true>(kp, p.k_str[2], k0, p.Lk, p.D, Ks, Kt, tid);
+    load_tile<T, DP, BN, SK, ST, false>(vp, p.v_str[2], k0, p.Lk, p.D, Vs, nullptr, tid);
+    __syncthreads();
+
+    f32x16 s[2], dp[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[kb][r] = 0.f;
+        dp[kb][r] = 0.f;
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int off = (kb * 32 + c32) * SK + c * KC + g * EPC;
+        M::run(s[kb], ld16(&Ks[off]), qf[c]);
+        M::run(dp[kb], ld16(&Vs[off]), df[c]);
+      }
+    }
+
+    const bool need_mask = p.has_mask && !(cls & 2);
+    const bool diag = p.causal && (k0 + BN - 1 > qw0);
+    const bool tail = k0 + BN > p.Lk;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int key0 = k0 + kb * 32 + 8 * c + 4 * g;
+        f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+        if (p.has_bias) bv = load_bias4(p, p.bias, brow + key0, p.Lk - key0);
+        uint32_t mw = 0x01010101u;
+        if (need_mask) mw = load_mask4(p, mrow + key0, p.Lk - key0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int kk = key0 + j;
+          float x = s[kb][4 * c + j] * p.scale_log2;
+          x = __builtin_fmaf(bv[j], kLog2e, x);
+          bool keep = mask_bit(mw, j) && qok;
+          if (tail) keep = keep && kk < p.Lk;
+          if (diag) keep = keep && kk <= qrow;
+          const float pr = keep ? fast_exp2(x - lse2) : 0.f;
+          dp[kb][4 * c + j] = pr * (dp[kb][4 * c + j] - dlt);
+        }
+      }
+
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const T* row = &Kt[(db * 32 + c32) * ST];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int f = 0; f < FPB; ++f)
+          M::run(dq[db], lds_frag_t<T>(row + kb * 32, g, f), M::pack(dp[kb], f));
+    }
+  }
+
+  if (qok) {
+    T* dqp = (T*)p.dq + b * p.q_str[0] + h * p.q_str[1] + (int64_t)qrow * p.q_str[2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d0 = db * 32 + 8 * c + 4 * g;
+        if (d0 < p.D) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            dqp[d0 + j] = from_f32<T>(dq[db][4 * c + j] * p.scale);
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dbias reduction over broadcast batch / head axes (fp32 partials laid out
+// [B, H, LQ, Lk] -> out[OB, OH, LQ, Lk] in the bias dtype).  Deterministic:
+// each output element sums its partials in a fixed order.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void dbias_reduce_kernel(
+    const Params p, void* out, int64_t s0, int64_t s1, int64_t s2, int OB,
+    int OH, int LQ) {
+  const int64_t n = (int64_t)OB * OH * LQ * p.Lk;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int k = i % p.Lk;
+  int64_t t = i / p.Lk;
+  const int q = t % LQ;
+  t /= LQ;
+  const int oh = t % OH;
+  const int ob = t / OH;
+  const float* ws = reinterpret_cast<const float*>(p.dbias);
+  float acc = 0.f;
+  for (int b = (OB == 1 ? 0 : ob); b < (OB == 1 ? p.B : ob + 1); ++b)
+    for (int h = (OH == 1 ? 0 : oh); h < (OH == 1 ? p.H : oh + 1); ++h)
+      acc += ws[(((int64_t)b * p.H + h) * LQ + q) * p.Lk + k];
+  const int64_t off = ob * s0 + oh * s1 + q * s2 + k;
+  if (p.bias_dtype == kF32)
+    reinterpret_cast<float*>(out)[off] = acc;
+  else
+    reinterpret_cast<bf16*>(out)[off] = (bf16)acc;
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers.
+// ---------------------------------------------------------------------------
+void launch_delta(const Params& p, int io_dtype, hipStream_t stream) {
+  const int rows = p.B * p.H * p.Lq;
+  const int n = (rows + 15) / 16;
+  if (io_dtype == kBF16)
+    hipLaunchKernelGGL(delta_kernel<bf16>, dim3(n), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(delta_kernel<float>, dim3(n), dim3(256), 0, stream, p);
+}
+
+template <typename T, int DP>
+static void launch_dkdv_t(Params p, hipStream_t stream) {
+  p.nkt = (p.Lk + 127) / 128;
+  const int n = p.B * p.H * p.nkt;
+  hipLaunchKernelGGL((dkdv_kernel<T, DP>), dim3(n), dim3(256), 0, stream, p);
+}
+
+void launch_dkdv(const Params& p, int io_dtype, int dp, hipStream_t stream) {
+  if (io_dtype == kBF16) {
+    if (dp == 64) launch_dkdv_t<bf16, 64>(p, stream);
+    else launch_dkdv_t<bf16, 128>(p, stream);
+  } else {
+    if (dp == 64) launch_dkdv_t<float, 64>(p, stream);
+    else launch_dkdv_t<float, 128>(p, stream);
+  }
+}
+
+template <typename T, int DP>
+static void launch_dq_t(Params p, hipStream_t stream) {
+  p.nqt = (p.Lq + 127) / 128;
+  const int n = p.B * p.H * p.nqt;
+  hipLaunchKernelGGL((dq_kernel<T, DP>), dim3(n), dim3(256), 0, stream, p);
+}
+
+void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream) {
+  if (io_dtype == kBF16) {
+    if (dp == 64) launch_dq_t<bf16, 64>(p, stream);
+    else launch_dq_t<bf16, 128>(p, stream);
+  } else {
+    if (dp == 64) launch_dq_t<float, 64>(p, stream);
+    else launch_dq_t<float, 128>(p, stream);
+  }
+}
+
+void launch_dbias_reduce(const Params& p, void* out, const int64_t* out_str,
+                         int OB, int OH, int LQ, hipStream_t stream) {
+  const int64_t n = (int64_t)OB * OH * LQ * p.Lk;
+  const int nb = (int)((n + 255) / 256);
+  hipLaunchKernelGGL(dbias_reduce_kernel, dim3(nb), dim3(256), 0, stream, p,
+                     out, out_str[0], out_str[1], out_str[2], OB, OH, LQ);
+}
+
+}  // namespace nxa

@@ -1,0 +1,411 @@
+// C ABI of the attention library: descriptor validation, workspace layout,
+// kernel dispatch and the thread-local error message.  Declarations and the
+// reference interfaces each entry point replaces are in include/nxattn.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/nxattn.h"
+#include "nxa_launch.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+int esize(int dt) { return dt == NXA_BF16 ? 2 : 4; }
+
+// ---------------------------------------------------------------------------
+// Profiling: HIP events around each launch while enabled.
+// ---------------------------------------------------------------------------
+struct ProfRec {
+  std::string name;
+  hipEvent_t start, stop;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<ProfRec> g_prof;
+
+template <typename F>
+int launch(const char* name, hipStream_t stream, F&& f) {
+  bool on;
+  {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    on = g_prof_on;
+  }
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (on) {
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+      return fail(NXA_E_LAUNCH, "%s: hipEventCreate failed", name);
+    hipEventRecord(e0, stream);
+  }
+  f();
+  const hipError_t err = hipGetLastError();
+  if (on) {
+    hipEventRecord(e1, stream);
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    g_prof.push_back({name, e0, e1});
+  }
+  if (err != hipSuccess)
+    return fail(NXA_E_LAUNCH, "%s: launch failed: %s", name,
+                hipGetErrorString(err));
+  return NXA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Validation shared by every entry point.
+// ---------------------------------------------------------------------------
+int check_desc(const nxa_desc* d, int has_bias, int has_mask) {
+  if (!d) return fail(NXA_E_ARG, "descriptor is NULL");
+  if (d->io_dtype != NXA_BF16 && d->io_dtype != NXA_F32)
+    return fail(NXA_E_DTYPE, "io_dtype %d is not NXA_BF16 or NXA_F32",
+                d->io_dtype);
+  if (has_bias && d->bias_dtype != NXA_BF16 && d->bias_dtype != NXA_F32)
+    return fail(NXA_E_DTYPE, "bias_dtype %d is not NXA_BF16 or NXA_F32",
+                d->bias_dtype);
+  if (d->B <= 0 || d->H <= 0 || d->Lq <= 0 || d->Lk <= 0 || d->D <= 0)
+    return fail(NXA_E_SHAPE, "extents must be positive (B=%d H=%d Lq=%d Lk=%d D=%d)",
+                d->B, d->H, d->Lq, d->Lk, d->D);
+  const int epc = 16 / esize(d->io_dtype);
+  if (d->D > 128)
+    return fail(NXA_E_UNSUPPORTED, "head dim D=%d exceeds 128", d->D);
+  if (d->D % epc != 0)
+    return fail(NXA_E_UNSUPPORTED, "head dim D=%d must be a multiple of %d",
+                d->D, epc);
+  const int64_t rows = (int64_t)d->B * d->H * (int64_t)(d->Lq > d->Lk ? d->Lq : d->Lk);
+  if (rows >= (int64_t)1 << 31)
+    return fail(NXA_E_SHAPE, "B*H*L = %lld exceeds 2^31", (long long)rows);
+  const int64_t* strs[4] = {d->q_str, d->k_str, d->v_str, d->o_str};
+  const char* names[4] = {"q", "k", "v", "o"};
+  for (int t = 0; t < 4; ++t)
+    for (int i = 0; i < 3; ++i) {
+      if (strs[t][i] < 0)
+        return fail(NXA_E_LAYOUT, "%s stride %d is negative", names[t], i);
+      if (strs[t][i] % epc != 0)
+        return fail(NXA_E_LAYOUT,
+                    "%s stride %d (%lld) must be a multiple of %d elements",
+                    names[t], i, (long long)strs[t][i], epc);
+    }
+  if (has_bias)
+    for (int i = 0; i < 3; ++i)
+      if (d->bias_str[i] < 0)
+        return fail(NXA_E_LAYOUT, "bias stride %d is negative", i);
+  if (has_mask)
+    for (int i = 0; i < 3; ++i)
+      if (d->mask_str[i] < 0)
+        return fail(NXA_E_LAYOUT, "mask stride %d is negative", i);
+  return NXA_OK;
+}
+
+bool aligned(const void* p, size_t a) {
+  return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+struct MaskGeom {
+  int MB, MH, MQ, MK, rows;
+  size_t bytes;
+};
+
+MaskGeom mask_geom(const nxa_desc* d) {
+  MaskGeom m;
+  m.MB = (d->mask_str[0] == 0) ? 1 : d->B;
+  m.MH = (d->mask_str[1] == 0) ? 1 : d->H;
+  const bool qb = d->mask_str[2] == 0 || d->Lq == 1;
+  m.rows = qb ? 1 : d->Lq;
+  m.MQ = qb ? 1 : (d->Lq + nxa::kTile - 1) / nxa::kTile;
+  m.MK = (d->Lk + nxa::kTile - 1) / nxa::kTile;
+  m.bytes = (size_t)m.MB * m.MH * m.MQ * m.MK;
+  return m;
+}
+
+struct DbiasGeom {
+  int mode;        // nxa::DbiasMode
+  int LQ;          // rows of dbias: Lq (full) or 1 (column sum)
+  bool reduce;     // batch / head axes broadcast: fp32 partials + reduction
+  int OB, OH;
+  size_t partial_bytes;
+};
+
+DbiasGeom dbias_geom(const nxa_desc* d) {
+  DbiasGeom g;
+  const bool colsum = d->Lq > 1 && d->bias_str[2] == 0;
+  g.mode = colsum ? nxa::kDbiasColsum : nxa::kDbiasFull;
+  g.LQ = colsum ? 1 : d->Lq;
+  g.OB = d->bias_str[0] == 0 ? 1 : d->B;
+  g.OH = d->bias_str[1] == 0 ? 1 : d->H;
+  g.reduce = (d->B > 1 && g.OB == 1) || (d->H > 1 && g.OH == 1);
+  g.partial_bytes =
+      g.reduce ? (size_t)d->B * d->H * g.LQ * (size_t)d->Lk * sizeof(float) : 0;
+  return g;
+}
+
+struct WsLayout {
+  size_t tilemap, delta, partial, total;
+};
+
+WsLayout ws_layout(const nxa_desc* d, int has_bias, int has_mask, int is_bwd) {
+  WsLayout w{0, 0, 0, 0};
+  size_t off = 0;
+  if (has_mask) {
+    w.tilemap = off;
+    off += align256(mask_geom(d).bytes);
+  }
+  if (is_bwd) {
+    w.delta = off;
+    off += align256((size_t)d->B * d->H * d->Lq * sizeof(float));
+    if (has_bias) {
+      w.partial = off;
+      off += align256(dbias_geom(d).partial_bytes);
+    }
+  }
+  w.total = off;
+  return w;
+}
+
+nxa::Params base_params(const nxa_desc* d, const void* q, const void* k,
+                        const void* v, const void* bias, const uint8_t* mask) {
+  nxa::Params p;
+  std::memset(&p, 0, sizeof(p));
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.bias = bias;
+  p.mask = mask;
+  for (int i = 0; i < 3; ++i) {
+    p.q_str[i] = d->q_str[i];
+    p.k_str[i] = d->k_str[i];
+    p.v_str[i] = d->v_str[i];
+    p.o_str[i] = d->o_str[i];
+    p.bias_str[i] = bias ? d->bias_str[i] : 0;
+    p.mask_str[i] = mask ? d->mask_str[i] : 0;
+  }
+  p.B = d->B;
+  p.H = d->H;
+  p.Lq = d->Lq;
+  p.Lk = d->Lk;
+  p.D = d->D;
+  p.scale = d->scale;
+  p.scale_log2 = d->scale * nxa::kLog2e;
+  p.causal = d->causal ? 1 : 0;
+  p.has_bias = bias != nullptr;
+  p.bias_dtype = d->bias_dtype;
+  if (bias) {
+    const int bes = esize(d->bias_dtype);
+    bool vec = (d->Lk % 4 == 0) && aligned(bias, 4 * bes);
+    for (int i = 0; i < 3; ++i) vec = vec && (d->bias_str[i] % 4 == 0);
+    p.bias_vec = vec;
+  }
+  p.has_mask = mask != nullptr;
+  if (mask) {
+    bool vec = (d->Lk % 4 == 0) && aligned(mask, 4);
+    for (int i = 0; i < 3; ++i) vec = vec && (d->mask_str[i] % 4 == 0);
+    p.mask_vec = vec;
+  }
+  return p;
+}
+
+// Writes (or just binds) the tile map for `mask` into the workspace.
+int setup_tilemap(nxa::Params& p, const nxa_desc* d, uint8_t* tm, bool build,
+                  hipStream_t stream) {
+  const MaskGeom m = mask_geom(d);
+  p.has_tilemap = 1;
+  p.tilemap = tm;
+  p.tilemap_out = tm;
+  p.tm_rows = m.rows;
+  p.tm_nk = m.MK;
+  p.tm_str[0] = m.MB > 1 ? (int64_t)m.MH * m.MQ * m.MK : 0;
+  p.tm_str[1] = m.MH > 1 ? (int64_t)m.MQ * m.MK : 0;
+  p.tm_str[2] = m.MQ > 1 ? m.MK : 0;
+  if (!build) return NXA_OK;
+  bool vec16 = aligned(p.mask, 16);
+  for (int i = 0; i < 3; ++i) vec16 = vec16 && (p.mask_str[i] % 16 == 0);
+  if (m.bytes >= ((size_t)1 << 31))
+    return fail(NXA_E_SHAPE, "mask tile map has %zu tiles (limit 2^31)", m.bytes);
+  return launch("tilemap", stream, [&] {
+    nxa::launch_tilemap(p, m.MB, m.MH, m.MQ, m.MK, vec16 ? 1 : 0, stream);
+  });
+}
+
+int check_io_ptrs(const nxa_desc* d, const void* const* ptrs, const char* const* names,
+                  int n) {
+  for (int i = 0; i < n; ++i) {
+    if (!ptrs[i]) return fail(NXA_E_ARG, "%s is NULL", names[i]);
+    if (!aligned(ptrs[i], 16))
+      return fail(NXA_E_LAYOUT, "%s is not 16-byte aligned", names[i]);
+  }
+  (void)d;
+  return NXA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nxa_version(void) { return NXA_VERSION; }
+
+const char* nxa_last_error(void) { return g_err.c_str(); }
+
+int nxa_check(const nxa_desc* desc, int has_bias, int has_mask) {
+  return check_desc(desc, has_bias, has_mask);
+}
+
+size_t nxa_workspace_bytes(const nxa_desc* desc, int has_bias, int has_mask,
+                           int is_bwd) {
+  if (check_desc(desc, has_bias, has_mask) != NXA_OK) return 0;
+  return ws_layout(desc, has_bias, has_mask, is_bwd).total;
+}
+
+int nxa_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
+            const void* bias, const uint8_t* mask, void* o, float* lse,
+            void* workspace, size_t workspace_bytes, void* stream_) {
+  int rc = check_desc(d, bias != nullptr, mask != nullptr);
+  if (rc) return rc;
+  const void* ptrs[4] = {q, k, v, o};
+  const char* names[4] = {"q", "k", "v", "o"};
+  if ((rc = check_io_ptrs(d, ptrs, names, 4))) return rc;
+  const WsLayout ws = ws_layout(d, bias != nullptr, mask != nullptr, 0);
+  if (ws.total > 0 && (!workspace || workspace_bytes < ws.total))
+    return fail(NXA_E_WORKSPACE, "forward needs %zu workspace bytes, got %zu",
+                ws.total, workspace ? workspace_bytes : (size_t)0);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  nxa::Params p = base_params(d, q, k, v, bias, mask);
+  p.o = o;
+  p.lse = lse;
+  if (mask) {
+    rc = setup_tilemap(p, d, static_cast<uint8_t*>(workspace) + ws.tilemap, true,
+                       stream);
+    if (rc) return rc;
+  }
+  const int dp = d->D <= 64 ? 64 : 128;
+  return launch("fwd", stream, [&] { nxa::launch_fwd(p, d->io_dtype, dp, stream); });
+}
+
+int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
+            const void* bias, const uint8_t* mask, const void* o,
+            const float* lse, const void* dout, void* dq, void* dk, void* dv,
+            void* dbias, const int64_t* dbias_str, void* workspace,
+            size_t workspace_bytes, int tilemap_ready, void* stream_) {
+  int rc = check_desc(d, bias != nullptr, mask != nullptr);
+  if (rc) return rc;
+  const void* ptrs[8] = {q, k, v, o, dout, dq, dk, dv};
+  const char* names[8] = {"q", "k", "v", "o", "dout", "dq", "dk", "dv"};
+  if ((rc = check_io_ptrs(d, ptrs, names, 8))) return rc;
+  if (!lse) return fail(NXA_E_ARG, "lse is NULL");
+  if (dbias && !bias) return fail(NXA_E_ARG, "dbias requested without a bias");
+  if (dbias && !dbias_str) return fail(NXA_E_ARG, "dbias_str is NULL");
+  // dK / dV are written once per (b, h): broadcast k / v cannot take them.
+  for (int i = 0; i < 2; ++i) {
+    const int ext = i == 0 ? d->B : d->H;
+    if (ext > 1 && (d->k_str[i] == 0 || d->v_str[i] == 0))
+      return fail(NXA_E_UNSUPPORTED,
+                  "backward needs k / v materialised over axis %d (stride 0)", i);
+    if (ext > 1 && d->q_str[i] == 0)
+      return fail(NXA_E_UNSUPPORTED,
+                  "backward needs q materialised over axis %d (stride 0)", i);
+  }
+  const WsLayout ws = ws_layout(d, bias != nullptr, mask != nullptr, 1);
+  if (!workspace || workspace_bytes < ws.total)
+    return fail(NXA_E_WORKSPACE, "backward needs %zu workspace bytes, got %zu",
+                ws.total, workspace ? workspace_bytes : (size_t)0);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  uint8_t* wsb = static_cast<uint8_t*>(workspace);
+  nxa::Params p = base_params(d, q, k, v, bias, mask);
+  p.o = const_cast<void*>(o);
+  p.lse = const_cast<float*>(lse);
+  p.dout = dout;
+  p.dq = dq;
+  p.dk = dk;
+  p.dv = dv;
+  p.delta = reinterpret_cast<float*>(wsb + ws.delta);
+  if ((rc = launch("delta", stream,
+                   [&] { nxa::launch_delta(p, d->io_dtype, stream); })))
+    return rc;
+  if (mask) {
+    rc = setup_tilemap(p, d, wsb + ws.tilemap, !tilemap_ready, stream);
+    if (rc) return rc;
+  }
+  DbiasGeom dg{};
+  if (dbias) {
+    dg = dbias_geom(d);
+    p.dbias_mode = dg.mode;
+    if (dg.reduce) {
+      p.dbias = wsb + ws.partial;
+      p.dbias_f32 = 1;
+      p.dbias_str[0] = (int64_t)d->H * dg.LQ * d->Lk;
+      p.dbias_str[1] = (int64_t)dg.LQ * d->Lk;
+      p.dbias_str[2] = dg.mode == nxa::kDbiasFull ? d->Lk : 0;
+    } else {
+      p.dbias = dbias;
+      for (int i = 0; i < 3; ++i) p.dbias_str[i] = dbias_str[i];
+    }
+  }
+  const int dp = d->D <= 64 ? 64 : 128;
+  if ((rc = launch("dkdv", stream,
+                   [&] { nxa::launch_dkdv(p, d->io_dtype, dp, stream); })))
+    return rc;
+  if ((rc = launch("dq", stream, [&] { nxa::launch_dq(p, d->io_dtype, dp, stream); })))
+    return rc;
+  if (dbias && dg.reduce) {
+    rc = launch("dbias_reduce", stream, [&] {
+      nxa::launch_dbias_reduce(p, dbias, dbias_str, dg.OB, dg.OH, dg.LQ, stream);
+    });
+    if (rc) return rc;
+  }
+  return NXA_OK;
+}
+
+int nxa_profile_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof_on = on != 0;
+  return NXA_OK;
+}
+
+int nxa_profile_read(const char* kernel, double* total_ms, int64_t* launches) {
+  if (!kernel || !total_ms || !launches)
+    return fail(NXA_E_ARG, "nxa_profile_read: NULL argument");
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  double tot = 0.0;
+  int64_t n = 0;
+  const size_t kl = std::strlen(kernel);
+  for (auto& r : g_prof) {
+    if (r.name.compare(0, kl, kernel) != 0) continue;
+    if (hipEventSynchronize(r.stop) != hipSuccess)
+      return fail(NXA_E_LAUNCH, "nxa_profile_read: event wait failed");
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess)
+      return fail(NXA_E_LAUNCH, "nxa_profile_read: elapsed time failed");
+    tot += ms;
+    ++n;
+  }
+  *total_ms = tot;
+  *launches = n;
+  return NXA_OK;
+}
+
+int nxa_profile_reset(void) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  for (auto& r : g_prof) {
+    hipEventDestroy(r.start);
+    hipEventDestroy(r.stop);
+  }
+  g_prof.clear();
+  return NXA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,265 @@
+// Shared device-side definitions for the gfx950 attention kernels.
+//
+// Conventions used by every kernel in this library
+// ------------------------------------------------
+// * Tensors are [B, H, L, D] with unit stride over D; the B/H/L strides come
+//   from the descriptor (element units).  Bias and mask are [B, H, Lq, Lk]
+//   with unit stride over Lk and zero strides on broadcast axes.
+// * Matrix products run on 32x32 MFMA tiles (v_mfma_f32_32x32x16_bf16 for
+//   bf16 I/O, v_mfma_f32_32x32x2_f32 for fp32 I/O), fp32 accumulation.
+// * A lane's 16-byte operand chunk c covers head-dim elements
+//   d = c*KC + g*EPC + [0, EPC) where g = lane / 32, EPC = elements per 16 B
+//   and KC = 2*EPC.  A and B operands use the same mapping, so any fixed
+//   permutation of the reduction index is harmless.
+// * 32x32 accumulator layout: lane l holds column (l % 32) and rows
+//   8*(r/4) + 4*(l/32) + (r%4) for register r in [0, 16).
+// * When an accumulator feeds the next product as its reduction operand
+//   (P into P.V, dS into dS.K, ...), register group c (registers 4c..4c+3)
+//   maps to reduction rows 8c + 4g + [0, 4); the transposed LDS copy of the
+//   other operand is read at exactly those rows.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nxa {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kTile = 64;  // tile-map granularity (queries x keys)
+
+enum DType : int { kBF16 = 0, kF32 = 1 };
+
+// dbias handling selected on the host.
+enum DbiasMode : int {
+  kDbiasNone = 0,
+  kDbiasFull = 1,      // dbias has the full [Lq, Lk] extent per (b, h): store dS
+  kDbiasColsum = 2,    // bias broadcast over Lq: store sum_q dS per key
+};
+
+// All kernels take one parameter block by value.
+struct Params {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* bias;
+  const uint8_t* mask;
+  void* o;
+  float* lse;
+  const void* dout;
+  void* dq;
+  void* dk;
+  void* dv;
+  void* dbias;         // final dbias, or the fp32 partial buffer (dbias_f32=1)
+  float* delta;
+  const uint8_t* tilemap;
+  uint8_t* tilemap_out;
+
+  int64_t q_str[3], k_str[3], v_str[3], o_str[3];  // B, H, L (D stride is 1)
+  int64_t bias_str[3];                               // B, H, Lq (Lk stride 1)
+  int64_t mask_str[3];
+  int64_t dbias_str[3];
+  int64_t tm_str[3];                                 // tile-map B, H, Q-tile
+
+  int B, H, Lq, Lk, D;
+  int nqt;             // query tiles of the launching kernel (grid decode)
+  int nkt;             // key tiles of the launching kernel
+  float scale;
+  float scale_log2;    // scale * log2(e)
+  int causal;
+  int has_bias, bias_dtype, bias_vec;
+  int has_mask, mask_vec;
+  int has_tilemap;
+  int tm_nk;           // tile-map key tiles
+  int tm_rows;         // mask rows covered by the tile map (Lq, or 1 if broadcast)
+  int dbias_mode;
+  int dbias_f32;       // 1: dbias points at fp32 partials, else bias dtype
+};
+
+// ---------------------------------------------------------------------------
+// MFMA policy per I/O type.
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Mma;
+
+template <>
+struct Mma<bf16> {
+  static constexpr int EPC = 8;   // elements per 16-byte chunk
+  static constexpr int KC = 16;   // reduction elements per chunk (both lane groups)
+  using Frag = bf16x8;
+  static __device__ __forceinline__ void run(f32x16& c, const Frag& a,
+                                             const Frag& b) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  // Reduction fragment f of a 32-row accumulator block: registers 8f..8f+7
+  // (row groups c = 2f, 2f+1).
+  static constexpr int FRAGS_PER_BLOCK = 2;
+  static __device__ __forceinline__ Frag pack(const f32x16& acc, int f) {
+    Frag r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = (bf16)acc[8 * f + j];
+    return r;
+  }
+};
+
+template <>
+struct Mma<float> {
+  static constexpr int EPC = 4;
+  static constexpr int KC = 8;
+  using Frag = f32x4;
+  static __device__ __forceinline__ void run(f32x16& c, const Frag& a,
+                                             const Frag& b) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], c, 0, 0, 0);
+  }
+  static constexpr int FRAGS_PER_BLOCK = 4;
+  static __device__ __forceinline__ Frag pack(const f32x16& acc, int f) {
+    Frag r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = acc[4 * f + j];
+    return r;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Memory helpers.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::Frag ld16(const T* p) {
+  return *reinterpret_cast<const typename Mma<T>::Frag*>(p);
+}
+
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::Frag zero_frag() {
+  typename Mma<T>::Frag z;
+#pragma unroll
+  for (int j = 0; j < Mma<T>::EPC; ++j) z[j] = (T)0.0f;
+  return z;
+}
+
+// Transposed-operand fragment f from an LDS row holding reduction index as
+// the contiguous axis: row groups c = f*(EPC/4) + i read 4 elements at
+// row[8c + 4g].
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::Frag lds_frag_t(const T* row,
+                                                            int g, int f);
+
+template <>
+__device__ __forceinline__ bf16x8 lds_frag_t<bf16>(const bf16* row, int g,
+                                                   int f) {
+  const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + 16 * f + 4 * g);
+  const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 16 * f + 8 + 4 * g);
+  bf16x8 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    r[j] = lo[j];
+    r[4 + j] = hi[j];
+  }
+  return r;
+}
+
+template <>
+__device__ __forceinline__ f32x4 lds_frag_t<float>(const float* row, int g,
+                                                   int f) {
+  return *reinterpret_cast<const f32x4*>(row + 8 * f + 4 * g);
+}
+
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(float x) { return x; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x) {
+  return (T)x;
+}
+
+// Four contiguous bias values (as fp32), honouring the runtime dtype.
+__device__ __forceinline__ f32x4 load_bias4(const Params& p, const void* base,
+                                            int64_t off, int valid) {
+  f32x4 r = {0.f, 0.f, 0.f, 0.f};
+  if (p.bias_dtype == kBF16) {
+    const bf16* b = reinterpret_cast<const bf16*>(base) + off;
+    if (p.bias_vec && valid >= 4) {
+      const bf16x4 v = *reinterpret_cast<const bf16x4*>(b);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r[j] = (float)v[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j < valid) r[j] = (float)b[j];
+    }
+  } else {
+    const float* b = reinterpret_cast<const float*>(base) + off;
+    if (p.bias_vec && valid >= 4) {
+      r = *reinterpret_cast<const f32x4*>(b);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j < valid) r[j] = b[j];
+    }
+  }
+  return r;
+}
+
+// Four contiguous keep-mask bytes packed into the low bits of each byte
+// (nonzero = keep); entries past `valid` read as masked.
+__device__ __forceinline__ uint32_t load_mask4(const Params& p, const uint8_t* m,
+                                               int valid) {
+  if (p.mask_vec && valid >= 4) return *reinterpret_cast<const uint32_t*>(m);
+  uint32_t r = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (j < valid) r |= (uint32_t)m[j] << (8 * j);
+  return r;
+}
+
+__device__ __forceinline__ bool mask_bit(uint32_t w, int j) {
+  return ((w >> (8 * j)) & 0xffu) != 0;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+
+__device__ __forceinline__ float shfl_xor32(float x) {
+  return __shfl_xor(x, 32, 64);
+}
+
+// Tile-map lookup: bit0 = some entry kept, bit1 = every entry kept.
+__device__ __forceinline__ int tile_class(const Params& p, int b, int h,
+                                          int q_lo, int q_hi, int k_lo,
+                                          int k_hi) {
+  // [q_lo, q_hi) x [k_lo, k_hi) in element units; clipped to the mask extent.
+  const uint8_t* tm = p.tilemap + b * p.tm_str[0] + h * p.tm_str[1];
+  int any = 0, all = 1;
+  const int qt0 = p.tm_rows == 1 ? 0 : q_lo / kTile;
+  const int qt1 = p.tm_rows == 1 ? 0 : (min(q_hi, p.Lq) - 1) / kTile;
+  const int kt0 = k_lo / kTile;
+  const int kt1 = (min(k_hi, p.Lk) - 1) / kTile;
+  for (int qt = qt0; qt <= qt1; ++qt)
+    for (int kt = kt0; kt <= kt1; ++kt) {
+      const int c = tm[qt * p.tm_str[2] + kt];
+      any |= c & 1;
+      all &= (c >> 1) & 1;
+    }
+  return any | (all << 1);
+}
+
+// Maps a linear block id so that consecutive virtual ids land on the same
+// XCD (blocks are dispatched round-robin over the 8 XCDs): blocks that share
+// K/V (same batch and head) then share one L2.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  constexpr int kXcd = 8;
+  if (nblocks % kXcd != 0) return bid;
+  return (bid % kXcd) * (nblocks / kXcd) + bid / kXcd;
+}
+
+}  // namespace nxa

@@ -1,0 +1,259 @@
+"""Parity of the fused gfx950 path against the CPU oracle (GPU only).
+
+Every case runs the public drop-in (``scaled_dot_product_attention(...,
+backend='hip')``, which calls ``nxa_fwd`` / ``nxa_bwd`` through the C ABI)
+on seeded inputs and compares it with the float64 oracle on the same values:
+
+* bf16 I/O: the oracle sees the bf16-rounded inputs upcast to float; the
+  budget is ``max|a-b| / max|b| <= 2e-2`` for the output and every gradient;
+* fp32 I/O: ``<= 1e-5`` for the output and the gradients.
+
+Cases mirror the reference's fused-path tests
+(``tests/test_nn_attention_kernel.py:60-140``: dense / bias / causal / mask /
+cross, grads incl. dbias) and add what this kernel must get right: tails
+(lengths that are not tile multiples), head dims below the padded width,
+every bias broadcast pattern, key-padding / random / block-sparse masks,
+causal with s != t, and fully masked rows (NaN, as the reference).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from _golden import ATTENTION_CASES, CROSS_ATOL, TOL, load_golden, relerr
+
+from oracle import attention as O
+
+pytestmark = pytest.mark.gpu
+
+REL = {torch.bfloat16: 2e-2, torch.float32: 1e-5}
+
+
+def _dev():
+    return torch.device('cuda:0')
+
+
+def _draw(rng, shape, dtype):
+    x = rng.standard_normal(shape).astype(np.float32)
+    if dtype == torch.bfloat16:
+        x = O.round_bf16(x)
+    return x
+
+
+def _to(x, dtype, req=False):
+    t = torch.from_numpy(np.ascontiguousarray(x)).to(_dev(), dtype)
+    return t.requires_grad_(req)
+
+
+def _make_mask(rng, kind, B, H, s, t):
+    if kind is None:
+        return None
+    if kind == 'keypad':
+        valid = rng.integers(1, t + 1, size=B)
+        m = np.arange(t)[None, :] < valid[:, None]
+        return m[:, None, None, :]
+    if kind == 'random':
+        m = rng.random((B, H, s, t)) < 0.6
+        m[..., 0] = True
+        return m
+    if kind == 'block':
+        nbq, nbk = -(-s // 64), -(-t // 64)
+        blk = rng.random((nbq, nbk)) < 0.35
+        for i in range(min(nbq, nbk)):
+            blk[i, i] = True
+        m = np.kron(blk, np.ones((64, 64), bool))[:s, :t]
+        m[:, 0] = True
+        return m[None, None]
+    if kind == 'rowbcast':
+        m = rng.random((1, H, 1, t)) < 0.5
+        m[..., 0] = True
+        return m
+    raise ValueError(kind)
+
+
+def _check(dtype, B, H, s, t, d, *, bias_shape=None, bias_dtype=None,
+           mask_kind=None, causal=False, seed=0, grads=True):
+    rng = np.random.default_rng(seed)
+    q = _draw(rng, (B, H, s, d), dtype)
+    k = _draw(rng, (B, H, t, d), dtype)
+    v = _draw(rng, (B, H, t, d), dtype)
+    bdt = bias_dtype or dtype
+    bias = None if bias_shape is None else _draw(rng, bias_shape, bdt)
+    mask = _make_mask(rng, mask_kind, B, H, s, t)
+    g = _draw(rng, (B, H, s, d), dtype)
+    scale = 1.0 / np.sqrt(d)
+
+    tq, tk, tv = _to(q, dtype, grads), _to(k, dtype, grads), _to(v, dtype, grads)
+    tb = None if bias is None else _to(bias, bdt, grads)
+    tm = None if mask is None else torch.from_numpy(mask).to(_dev())
+    from nitrix_amd import scaled_dot_product_attention
+
+    print(f'[case] {dtype} B{B} H{H} s{s} t{t} d{d} bias={bias_shape} '
+          f'mask={mask_kind} causal={causal} seed={seed}', flush=True)
+    out = scaled_dot_product_attention(
+        tq, tk, tv, bias=tb, mask=tm, causal=causal, backend='hip'
+    )
+    ref = O.sdpa_forward(q, k, v, bias=bias, mask=mask, scale=scale,
+                         causal=causal, acc_dtype=np.float64)
+    tol = REL[dtype]
+    got = out.detach().float().cpu().numpy()
+    assert got.shape == ref.shape
+    assert np.all(np.isfinite(got)), 'unexpected non-finite output'
+    err = relerr(got, ref)
+    assert err <= tol, f'out relerr {err:.3e} > {tol}'
+    if not grads:
+        return
+    out.backward(_to(g, dtype))
+    torch.cuda.synchronize()
+    dq, dk, dv, db = O.sdpa_backward(q, k, v, g, bias=bias, mask=mask,
+                                     scale=scale, causal=causal,
+                                     acc_dtype=np.float64)
+    pairs = [('dq', tq.grad, dq), ('dk', tk.grad, dk), ('dv', tv.grad, dv)]
+    if bias is not None:
+        pairs.append(('dbias', tb.grad, db))
+    for name, got_t, want in pairs:
+        assert got_t is not None, name
+        got = got_t.float().cpu().numpy()
+        assert got.shape == want.shape, (name, got.shape, want.shape)
+        e = relerr(got, want)
+        assert e <= tol, f'{name} relerr {e:.3e} > {tol}'
+
+
+DTYPES = [torch.bfloat16, torch.float32]
+
+
+@pytest.mark.parametrize('dtype', DTYPES, ids=['bf16', 'f32'])
+@pytest.mark.parametrize('d', [64, 128])
+def test_dense(dtype, d):
+    _check(dtype, 2, 2, 256, 256, d)
+
+
+@pytest.mark.parametrize('dtype', DTYPES, ids=['bf16', 'f32'])
+@pytest.mark.parametrize('s,t,d', [(100, 77, 64), (33, 200, 128), (6, 9, 8),
+                                   (130, 129, 40), (1, 65, 64)])
+def test_tails_and_padded_head_dim(dtype, s, t, d):
+    _check(dtype, 2, 3, s, t, d, seed=s + t)
+
+
+@pytest.mark.parametrize('dtype', DTYPES, ids=['bf16', 'f32'])
+@pytest.mark.parametrize('s,t', [(256, 256), (200, 130), (96, 300)])
+def test_causal(dtype, s, t):
+    _check(dtype, 2, 2, s, t, 64, causal=True, seed=3)
+
+
+@pytest.mark.parametrize('dtype', DTYPES, ids=['bf16', 'f32'])
+@pytest.mark.parametrize('bias_shape', [
+    (2, 2, 192, 160),   # full
+    (2, 192, 160),      # shared over batch (the windowed-bias fixture pattern)
+    (1, 2, 1, 160),     # query-broadcast (distance / ALiBi-style column bias)
+    (192, 160),         # shared over batch and heads
+    (2, 1, 192, 160),   # shared over heads
+], ids=['full', 'batchbc', 'qbc', 'bhbc', 'headbc'])
+def test_bias_broadcast(dtype, bias_shape):
+    _check(dtype, 2, 2, 192, 160, 64, bias_shape=bias_shape, seed=5)
+
+
+def test_bias_fp32_with_bf16_io():
+    _check(torch.bfloat16, 2, 2, 128, 128, 64, bias_shape=(2, 2, 128, 128),
+           bias_dtype=torch.float32, seed=6)
+
+
+@pytest.mark.parametrize('dtype', DTYPES, ids=['bf16', 'f32'])
+@pytest.mark.parametrize('kind', ['keypad', 'random', 'block', 'rowbcast'])
+def test_masks(dtype, kind):
+    _check(dtype, 2, 2, 320, 256, 64, mask_kind=kind, seed=7)
+
+
+def test_mask_bias_causal_combined():
+    _check(torch.bfloat16, 2, 2, 300, 300, 128, bias_shape=(2, 300, 300),
+           mask_kind='random', causal=True, seed=8)
+
+
+def test_fully_masked_row_is_nan():
+    rng = np.random.default_rng(9)
+    q = _draw(rng, (1, 2, 70, 64), torch.bfloat16)
+    k = _draw(rng, (1, 2, 90, 64), torch.bfloat16)
+    v = _draw(rng, (1, 2, 90, 64), torch.bfloat16)
+    mask = rng.random((1, 2, 70, 90)) < 0.5
+    mask[..., 0] = True
+    mask[0, 1, 5] = False
+    mask[0, 0, 69] = False
+    from nitrix_amd import scaled_dot_product_attention
+
+    out = scaled_dot_product_attention(
+        _to(q, torch.bfloat16), _to(k, torch.bfloat16), _to(v, torch.bfloat16),
+        mask=torch.from_numpy(mask).to(_dev()), backend='hip',
+    ).float().cpu().numpy()
+    ref = O.sdpa_forward(q, k, v, mask=mask, acc_dtype=np.float64)
+    assert np.all(np.isnan(out[0, 1, 5])) and np.all(np.isnan(out[0, 0, 69]))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(np.isnan(out), ~ok)
+    assert relerr(out[ok], ref[ok]) <= 2e-2
+
+
+@pytest.mark.parametrize('name', ATTENTION_CASES)
+def test_reference_golden_fixtures_fp32(name):
+    """The reference's own fixtures through the fused fp32 path (d=8, s=6,
+    t=6/9: head-dim padding and length tails)."""
+    from nitrix_amd import scaled_dot_product_attention
+
+    data = load_golden(name)
+    kw = {}
+    if 'bias' in data:
+        kw['bias'] = _to(data['bias'], torch.float32)
+    out = scaled_dot_product_attention(
+        _to(data['q'], torch.float32),
+        _to(data['k'], torch.float32),
+        _to(data['v'], torch.float32),
+        causal=bool(data['causal']),
+        qk_norm=bool(data['qk_norm']) if 'qk_norm' in data else False,
+        backend='hip',
+        **kw,
+    ).cpu().numpy()
+    if name == 'attention_cross_float32':
+        np.testing.assert_allclose(out, data['out'], atol=CROSS_ATOL, rtol=0)
+    else:
+        atol, rtol = TOL[('attention', 'float32')]
+        np.testing.assert_allclose(out, data['out'], atol=atol, rtol=rtol)
+
+
+def test_leading_batch_dims_and_broadcast_kv():
+    """``(..., h, s, d)`` with two leading axes; k / v broadcast over one of
+    them (zero strides in the forward, materialised for the backward)."""
+    rng = np.random.default_rng(10)
+    dtype = torch.bfloat16
+    q = _draw(rng, (2, 3, 2, 64, 64), dtype)
+    k = _draw(rng, (1, 3, 2, 80, 64), dtype)
+    v = _draw(rng, (1, 3, 2, 80, 64), dtype)
+    g = _draw(rng, (2, 3, 2, 64, 64), dtype)
+    tq, tk, tv = _to(q, dtype, True), _to(k, dtype, True), _to(v, dtype, True)
+    from nitrix_amd import scaled_dot_product_attention
+
+    out = scaled_dot_product_attention(tq, tk, tv, backend='hip')
+    out.backward(_to(g, dtype))
+    kb = np.broadcast_to(k, q.shape[:-2] + k.shape[-2:])
+    vb = np.broadcast_to(v, q.shape[:-2] + v.shape[-2:])
+    ref = O.sdpa_forward(q, kb, vb, acc_dtype=np.float64)
+    dq, dk, dv, _ = O.sdpa_backward(q, kb, vb, g, acc_dtype=np.float64)
+    dk = O.unbroadcast(dk, k.shape)
+    dv = O.unbroadcast(dv, v.shape)
+    assert relerr(out.detach().float().cpu().numpy(), ref) <= 2e-2
+    for got, want in ((tq.grad, dq), (tk.grad, dk), (tv.grad, dv)):
+        assert got.shape == want.shape
+        assert relerr(got.float().cpu().numpy(), want) <= 2e-2
+
+
+def test_qk_norm_matches_oracle():
+    rng = np.random.default_rng(11)
+    dtype = torch.float32
+    q = _draw(rng, (2, 2, 50, 64), dtype) * 3
+    k = _draw(rng, (2, 2, 70, 64), dtype) * 3
+    v = _draw(rng, (2, 2, 70, 64), dtype)
+    from nitrix_amd import scaled_dot_product_attention
+
+    out = scaled_dot_product_attention(
+        _to(q, dtype), _to(k, dtype), _to(v, dtype), qk_norm=True, backend='hip'
+    ).cpu().numpy()
+    ref = O.sdpa_forward(q, k, v, qk_norm=True, acc_dtype=np.float64)
+    assert relerr(out, ref) <= 1e-5
