@@ -181,6 +181,22 @@ __device__ __forceinline__ T from_f32(float x) {
   return (T)x;
 }
 
+// Stores acc[off..off+3] * scale as four contiguous elements (8 or 16 bytes).
+__device__ __forceinline__ void store4(bf16* dst, const f32x16& acc, int off,
+                                       float scale) {
+  bf16x4 v;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = (bf16)(acc[off + j] * scale);
+  *reinterpret_cast<bf16x4*>(dst) = v;
+}
+__device__ __forceinline__ void store4(float* dst, const f32x16& acc, int off,
+                                       float scale) {
+  f32x4 v;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = acc[off + j] * scale;
+  *reinterpret_cast<f32x4*>(dst) = v;
+}
+
 // Four contiguous bias values (as fp32), honouring the runtime dtype.
 __device__ __forceinline__ f32x4 load_bias4(const Params& p, const void* base,
                                             int64_t off, int valid) {
