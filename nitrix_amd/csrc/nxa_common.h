@@ -173,6 +173,33 @@ __device__ __forceinline__ f32x4 lds_frag_t<float>(const float* row, int g,
   return *reinterpret_cast<const f32x4*>(row + 8 * f + 4 * g);
 }
 
+// Reduction-operand fragment f of a 32x16 MFMA operand read *transposed*
+// from a row-major bf16 LDS tile whose rows are the reduction index:
+// lane L receives tile[r0 + key(f, L/32, j)][col0 + L%32] for j = 0..7 with
+// key(f, g, j) = 16f + 8(j/4) + 4g + j%4 -- the row groups the accumulator
+// layout assigns to fragment f.
+//
+// ds_read_b64_tr_b16 works on 16-lane groups: output lane j, element e is
+// element (j%4) of the 8 bytes addressed by lane 4e + j/4 of the group.  So
+// lane i of a group addresses row (r0 + 16f + 4g + i/4 [+8]) at column
+// (col0 + 16*(group%2) + 4*(i%4)).
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8 lds_tr_frag(const bf16* tile, int stride,
+                                              int r0, int col0, int lane,
+                                              int f) {
+  const int grp = lane >> 4, i = lane & 15;
+  const int row = r0 + 16 * f + 4 * (grp >> 1) + (i >> 2);
+  const int col = col0 + 16 * (grp & 1) + 4 * (i & 3);
+  const bf16* p0 = tile + row * stride + col;
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
+  const i16x4 hi =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0 + 8 * stride));
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  const i16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
 __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
 __device__ __forceinline__ float to_f32(float x) { return x; }
 
