@@ -1,4 +1,6 @@
-// Backward pass: delta = rowsum(O * dO), then two deterministic kernels
+// Backward pass: delta = rowsum(O * dO), the fp32 dK/dV and dQ kernels (the
+// bf16 ones live in nxa_bwd_bf16.hip), the dbias reduction and the launchers.
+// Two deterministic kernels
 // (no atomics): dK/dV (+ dbias) with a grid over key tiles, and dQ with a
 // grid over query tiles.  Both recompute P from the forward's LSE.
 //
@@ -471,8 +473,7 @@ static void launch_dkdv_t(Params p, hipStream_t stream) {
 
 void launch_dkdv(const Params& p, int io_dtype, int dp, hipStream_t stream) {
   if (io_dtype == kBF16) {
-    if (dp == 64) launch_dkdv_t<bf16, 64>(p, stream);
-    else launch_dkdv_t<bf16, 128>(p, stream);
+    launch_dkdv_bf16(p, dp, stream);
   } else {
     if (dp == 64) launch_dkdv_t<float, 64>(p, stream);
     else launch_dkdv_t<float, 128>(p, stream);
@@ -488,8 +489,7 @@ static void launch_dq_t(Params p, hipStream_t stream) {
 
 void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream) {
   if (io_dtype == kBF16) {
-    if (dp == 64) launch_dq_t<bf16, 64>(p, stream);
-    else launch_dq_t<bf16, 128>(p, stream);
+    launch_dq_bf16(p, dp, stream);
   } else {
     if (dp == 64) launch_dq_t<float, 64>(p, stream);
     else launch_dq_t<float, 128>(p, stream);

@@ -1,0 +1,542 @@
+// bf16 backward kernels for gfx950: dK/dV (+ dbias) and dQ.
+//
+// Same math as the reference's two backward Pallas kernels
+// (src/nitrix/_kernels/cuda/attention.py:272-332 dK/dV, :335-387 dQ):
+// P = exp2(S * scale * log2e + bias * log2e - lse2), dS = P (dP - delta),
+// dV = P^T dO, dK = scale dS^T Q, dQ = scale dS K.  Deterministic (no
+// atomics): dK/dV own key tiles and stream query tiles, dQ owns query tiles
+// and streams key tiles.
+//
+// Layout choices for CDNA4:
+// * streamed tiles stay row-major in LDS; the transposed operands
+//   (dO^T, Q^T for dV/dK, K^T for dQ) come from ds_read_b64_tr_b16, so no
+//   transposed copies are written;
+// * row strides carry a 48-byte pad, conflict-free both for the 16-byte row
+//   reads of the S / dP products and for the transposed reads;
+// * the next tile is fetched into registers while the current one is
+//   consumed (double-buffered LDS, one barrier per tile);
+// * per-row LSE / delta are read as float4 for the four consecutive rows a
+//   lane's accumulator group covers.
+#include "nxa_common.h"
+#include "nxa_launch.h"
+
+namespace nxa {
+
+constexpr int kMaxBwdTiles = 1024;
+
+// dbias handling compiled into dK/dV.
+enum : int { kDbNone = 0, kDbFull = 1, kDbColsum = 2 };
+
+__device__ __forceinline__ void store_db(const Params& p, int64_t off, float x) {
+  if (p.dbias_f32 || p.bias_dtype == kF32)
+    reinterpret_cast<float*>(p.dbias)[off] = x;
+  else
+    reinterpret_cast<bf16*>(p.dbias)[off] = (bf16)x;
+}
+
+__device__ __forceinline__ float load_bias1(const Params& p, int64_t off) {
+  return p.bias_dtype == kBF16 ? (float)reinterpret_cast<const bf16*>(p.bias)[off]
+                               : reinterpret_cast<const float*>(p.bias)[off];
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV.  Block = 4 waves x 32 keys (128 keys); streams 64-query tiles.
+// Each wave computes S = Q K^T and dP = dO V^T with the key as the lane's
+// column, so P and dS feed dV^T = dO^T P and dK^T = Q^T dS from registers.
+// ---------------------------------------------------------------------------
+template <int DP, bool HAS_BIAS, bool CAUSAL, int DBM>
+__global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
+  using M = Mma<bf16>;
+  using Frag = bf16x8;
+  constexpr int EPC = 8, KC = 16;
+  constexpr int BNK = 128, BQ = 64;
+  constexpr int SQ = DP + 24;
+  constexpr int TSZ = BQ * SQ;
+  constexpr int NC = DP / KC, NDB = DP / 32, CPR = DP / EPC;
+  constexpr int NCH = BQ * CPR / 256;
+  constexpr int FPB = M::FRAGS_PER_BLOCK;
+  static_assert(NCH >= 1, "tile / block mismatch");
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TSZ];
+  __shared__ __attribute__((aligned(16))) float rows[2][2][BQ];
+  __shared__ uint8_t tcls[kMaxBwdTiles];
+
+  const int nblk = p.B * p.H * p.nkt;
+  const int vid = xcd_remap(blockIdx.x, nblk);
+  const int bh = vid / p.nkt;
+  const int kt = vid % p.nkt;
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, c32 = lane & 31;
+  const int kblk0 = kt * BNK;
+  const int kw0 = kblk0 + wave * 32;
+  const int key = kw0 + c32;
+  const bool kok = key < p.Lk;
+  const int kc = kok ? key : p.Lk - 1;
+
+  const bf16* qp = (const bf16*)p.q + b * p.q_str[0] + h * p.q_str[1];
+  const bf16* dop = (const bf16*)p.dout + b * p.o_str[0] + h * p.o_str[1];
+  const float* lsep = p.lse + ((int64_t)b * p.H + h) * p.Lq;
+  const float* dltp = p.delta + ((int64_t)b * p.H + h) * p.Lq;
+  const int64_t qs = p.q_str[2], os = p.o_str[2];
+
+  // Query-tile classes (0 = nothing kept for this key block).
+  const int nq = (p.Lq + BQ - 1) / BQ;
+  const bool cls_lds = nq <= kMaxBwdTiles;
+  auto tclass_g = [&](int t) -> int {
+    const int q0 = t * BQ;
+    if (CAUSAL && q0 + BQ - 1 < kblk0) return 0;
+    if (!p.has_tilemap) return 3;
+    return tile_class(p, b, h, q0, q0 + BQ, kblk0, kblk0 + BNK);
+  };
+  if (cls_lds)
+    for (int t = tid; t < nq; t += 256) tcls[t] = (uint8_t)tclass_g(t);
+  __syncthreads();
+  auto tclass = [&](int t) -> int { return cls_lds ? tcls[t] : tclass_g(t); };
+
+  // Stationary K / V fragments (B operands) for this lane's key.
+  Frag kf[NC], vf[NC];
+  {
+    const bf16* kp = (const bf16*)p.k + b * p.k_str[0] + h * p.k_str[1] +
+                     (int64_t)kc * p.k_str[2];
+    const bf16* vp = (const bf16*)p.v + b * p.v_str[0] + h * p.v_str[1] +
+                     (int64_t)kc * p.v_str[2];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = c * KC + g * EPC;
+      const bool ok = kok && d < p.D;
+      kf[c] = ok ? ld16(kp + d) : zero_frag<bf16>();
+      vf[c] = ok ? ld16(vp + d) : zero_frag<bf16>();
+    }
+  }
+  f32x16 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dk[db][r] = 0.f;
+      dv[db][r] = 0.f;
+    }
+  float colsum = 0.f;
+
+  // Bias: a per-key constant when it broadcasts over queries, else per row.
+  const bool bias_rows = HAS_BIAS && p.bias_str[2] != 0;
+  const int64_t bbase =
+      HAS_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] + kc : 0;
+  const float bkey = (HAS_BIAS && !bias_rows) ? load_bias1(p, bbase) * kLog2e : 0.f;
+  const uint8_t* mbase =
+      p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] + kc : nullptr;
+  const int64_t dbbase = b * p.dbias_str[0] + h * p.dbias_str[1] + key;
+
+  // Full dbias: entries of skipped tiles are zero.
+  if constexpr (DBM == kDbFull) {
+    if (kok)
+      for (int t = 0; t < nq; ++t)
+        if (!(tclass(t) & 1))
+          for (int i = 0; i < BQ && t * BQ + i < p.Lq; ++i)
+            store_db(p, dbbase + (int64_t)(t * BQ + i) * p.dbias_str[2], 0.f);
+  }
+
+  // --- streamed Q / dO tiles ---------------------------------------------------
+  Frag qst[NCH], dst[NCH];
+  float lst = 0.f, dlst = 0.f;
+  auto gload = [&](int q0) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int idx = tid + i * 256;
+      const int r = idx / CPR, d = (idx % CPR) * EPC;
+      const int q = q0 + r;
+      const bool ok = q < p.Lq && d < p.D;
+      qst[i] = ok ? ld16(qp + (int64_t)q * qs + d) : zero_frag<bf16>();
+      dst[i] = ok ? ld16(dop + (int64_t)q * os + d) : zero_frag<bf16>();
+    }
+    if (tid < BQ) {
+      const int q = q0 + tid;
+      lst = q < p.Lq ? lsep[q] * kLog2e : 0.f;
+      dlst = q < p.Lq ? dltp[q] : 0.f;
+    }
+  };
+  auto lstore = [&](int buf) {
+    bf16* Qs = smem + buf * 2 * TSZ;
+    bf16* Ds = Qs + TSZ;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int idx = tid + i * 256;
+      const int r = idx / CPR, d = (idx % CPR) * EPC;
+      *reinterpret_cast<Frag*>(&Qs[r * SQ + d]) = qst[i];
+      *reinterpret_cast<Frag*>(&Ds[r * SQ + d]) = dst[i];
+    }
+    if (tid < BQ) {
+      rows[buf][0][tid] = lst;
+      rows[buf][1][tid] = dlst;
+    }
+  };
+
+  int qt = 0;
+  while (qt < nq && !(tclass(qt) & 1)) ++qt;
+  if (qt < nq) {
+    gload(qt * BQ);
+    lstore(0);
+  }
+  __syncthreads();
+  int buf = 0;
+
+  while (qt < nq) {
+    const int cls = tclass(qt);
+    int qn = qt + 1;
+    while (qn < nq && !(tclass(qn) & 1)) ++qn;
+    if (qn < nq) gload(qn * BQ);
+
+    const bf16* Qs = smem + buf * 2 * TSZ;
+    const bf16* Ds = Qs + TSZ;
+    const float* lse2s = rows[buf][0];
+    const float* dlts = rows[buf][1];
+    const int q0 = qt * BQ;
+
+    f32x16 s[2], dp[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[qb][r] = 0.f;
+        dp[qb][r] = 0.f;
+      }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const int off = (qb * 32 + c32) * SQ + c * KC + g * EPC;
+        M::run(s[qb], ld16(&Qs[off]), kf[c]);
+        M::run(dp[qb], ld16(&Ds[off]), vf[c]);
+      }
+
+    const bool need_mask = p.has_mask && !(cls & 2);
+    const bool tail = (q0 + BQ > p.Lq) || (kw0 + 32 > p.Lk);
+    const bool diag = CAUSAL && (kw0 + 31 > q0);
+    const bool general = need_mask || tail || diag || bias_rows;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int ql0 = qb * 32 + 8 * c + 4 * g;
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&lse2s[ql0]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dlts[ql0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * c + j;
+          float x = __builtin_fmaf(s[qb][r], p.scale_log2, -l4[j]);
+          if constexpr (HAS_BIAS) x += bkey;
+          if (general) {
+            const int q = q0 + ql0 + j;
+            const int qcl = q < p.Lq ? q : p.Lq - 1;
+            if constexpr (HAS_BIAS)
+              if (bias_rows)
+                x = __builtin_fmaf(
+                    load_bias1(p, bbase + (int64_t)qcl * p.bias_str[2]), kLog2e, x);
+            bool keep = q < p.Lq && kok;
+            if (need_mask) keep = keep && mbase[(int64_t)qcl * p.mask_str[2]] != 0;
+            if (CAUSAL) keep = keep && key <= q;
+            x = keep ? x : -INFINITY;
+          }
+          const float pr = fast_exp2(x);
+          const float ds = pr * (dp[qb][r] - d4[j]);
+          s[qb][r] = pr;
+          dp[qb][r] = ds;
+          if constexpr (DBM == kDbFull) {
+            const int q = q0 + ql0 + j;
+            if (kok && q < p.Lq) store_db(p, dbbase + (int64_t)q * p.dbias_str[2], ds);
+          }
+          if constexpr (DBM == kDbColsum) colsum += ds;
+        }
+      }
+
+    // dV^T += dO^T P, dK^T += Q^T dS (transposed operands via ds_read_tr).
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int f = 0; f < FPB; ++f) {
+        const Frag pp = M::pack(s[qb], f);
+        const Frag pd = M::pack(dp[qb], f);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          M::run(dv[db], lds_tr_frag(Ds, SQ, qb * 32, db * 32, lane, f), pp);
+          M::run(dk[db], lds_tr_frag(Qs, SQ, qb * 32, db * 32, lane, f), pd);
+        }
+      }
+
+    if (qn < nq) lstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+    qt = qn;
+  }
+
+  if (kok) {
+    bf16* dkp = (bf16*)p.dk + b * p.k_str[0] + h * p.k_str[1] + (int64_t)key * p.k_str[2];
+    bf16* dvp = (bf16*)p.dv + b * p.v_str[0] + h * p.v_str[1] + (int64_t)key * p.v_str[2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d0 = db * 32 + 8 * c + 4 * g;
+        if (d0 < p.D) {
+          store4(dkp + d0, dk[db], 4 * c, p.scale);
+          store4(dvp + d0, dv[db], 4 * c, 1.0f);
+        }
+      }
+  }
+  if constexpr (DBM == kDbColsum) {
+    const float tot = colsum + shfl_xor32(colsum);
+    if (kok && g == 0) store_db(p, dbbase, tot);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ.  Block = 4 waves x 32 queries (128); streams 64-key tiles in two
+// 32-key halves.  S^T = K Q^T and dP^T = V dO^T put the query on the lane's
+// column, so dS^T feeds dQ^T = K^T dS^T from registers; K^T is read
+// transposed from the row-major K tile.
+// ---------------------------------------------------------------------------
+template <int DP, bool HAS_BIAS, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
+  using M = Mma<bf16>;
+  using Frag = bf16x8;
+  constexpr int EPC = 8, KC = 16;
+  constexpr int BM = 128, BN = 64;
+  constexpr int SKT = DP + 24;  // K: row reads and transposed reads
+  constexpr int SKV = DP + 8;   // V: row reads only
+  constexpr int KSZ = BN * SKT, VSZ = BN * SKV;
+  constexpr int NC = DP / KC, NDB = DP / 32, CPR = DP / EPC;
+  constexpr int NCH = BN * CPR / 256;
+  constexpr int FPB = M::FRAGS_PER_BLOCK;
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * (KSZ + VSZ)];
+  __shared__ uint8_t tcls[kMaxBwdTiles];
+
+  const int nblk = p.B * p.H * p.nqt;
+  const int vid = xcd_remap(blockIdx.x, nblk);
+  const int bh = vid / p.nqt;
+  const int qt = p.nqt - 1 - (vid % p.nqt);
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, c32 = lane & 31;
+  const int q0 = qt * BM;
+  const int qw0 = q0 + wave * 32;
+  const int qrow = qw0 + c32;
+  const bool qok = qrow < p.Lq;
+  const int qc = qok ? qrow : p.Lq - 1;
+
+  const bf16* kp = (const bf16*)p.k + b * p.k_str[0] + h * p.k_str[1];
+  const bf16* vp = (const bf16*)p.v + b * p.v_str[0] + h * p.v_str[1];
+  const int64_t ks = p.k_str[2], vs = p.v_str[2];
+
+  const int k_end = CAUSAL ? min(p.Lk, q0 + BM) : p.Lk;
+  const int nkt = (k_end + BN - 1) / BN;
+  const bool cls_lds = p.has_tilemap && nkt <= kMaxBwdTiles;
+  if (cls_lds)
+    for (int t = tid; t < nkt; t += 256)
+      tcls[t] = (uint8_t)tile_class(p, b, h, q0, q0 + BM, t * BN, t * BN + BN);
+  __syncthreads();
+  auto tclass = [&](int t) -> int {
+    if (!p.has_tilemap) return 3;
+    if (cls_lds) return tcls[t];
+    return tile_class(p, b, h, q0, q0 + BM, t * BN, t * BN + BN);
+  };
+
+  Frag qf[NC], df[NC];
+  {
+    const bf16* qp = (const bf16*)p.q + b * p.q_str[0] + h * p.q_str[1] +
+                     (int64_t)qc * p.q_str[2];
+    const bf16* dop = (const bf16*)p.dout + b * p.o_str[0] + h * p.o_str[1] +
+                      (int64_t)qc * p.o_str[2];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = c * KC + g * EPC;
+      const bool ok = qok && d < p.D;
+      qf[c] = ok ? ld16(qp + d) : zero_frag<bf16>();
+      df[c] = ok ? ld16(dop + d) : zero_frag<bf16>();
+    }
+  }
+  const int64_t rowid = ((int64_t)b * p.H + h) * p.Lq + qc;
+  const float neg_lse2 = -p.lse[rowid] * kLog2e;
+  const float dlt = p.delta[rowid];
+  const int64_t brow = HAS_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] +
+                                      (int64_t)qc * p.bias_str[2]
+                                : 0;
+  const uint8_t* mrow = p.has_mask ? p.mask + b * p.mask_str[0] +
+                                         h * p.mask_str[1] +
+                                         (int64_t)qc * p.mask_str[2]
+                                   : nullptr;
+
+  f32x16 dq[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
+
+  Frag kst[NCH], vst[NCH];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int idx = tid + i * 256;
+      const int r = idx / CPR, d = (idx % CPR) * EPC;
+      const int key = k0 + r;
+      const bool ok = key < p.Lk && d < p.D;
+      kst[i] = ok ? ld16(kp + (int64_t)key * ks + d) : zero_frag<bf16>();
+      vst[i] = ok ? ld16(vp + (int64_t)key * vs + d) : zero_frag<bf16>();
+    }
+  };
+  auto lstore = [&](int buf) {
+    bf16* Ks = smem + buf * (KSZ + VSZ);
+    bf16* Vs = Ks + KSZ;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int idx = tid + i * 256;
+      const int r = idx / CPR, d = (idx % CPR) * EPC;
+      *reinterpret_cast<Frag*>(&Ks[r * SKT + d]) = kst[i];
+      *reinterpret_cast<Frag*>(&Vs[r * SKV + d]) = vst[i];
+    }
+  };
+
+  int kt = 0;
+  while (kt < nkt && !(tclass(kt) & 1)) ++kt;
+  if (kt < nkt) {
+    gload(kt * BN);
+    lstore(0);
+  }
+  __syncthreads();
+  int buf = 0;
+
+  while (kt < nkt) {
+    const int cls = tclass(kt);
+    int kn = kt + 1;
+    while (kn < nkt && !(tclass(kn) & 1)) ++kn;
+    if (kn < nkt) gload(kn * BN);
+
+    const bf16* Ks = smem + buf * (KSZ + VSZ);
+    const bf16* Vs = Ks + KSZ;
+    const int k0 = kt * BN;
+    const bool need_mask = p.has_mask && !(cls & 2);
+    const bool tail = k0 + BN > p.Lk;
+    const bool diag = CAUSAL && (k0 + BN - 1 > qw0);
+    const bool general = HAS_BIAS || need_mask || tail || diag;
+
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      f32x16 s, dpt;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = 0.f;
+        dpt[r] = 0.f;
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        M::run(s, ld16(&Ks[(kb * 32 + c32) * SKT + c * KC + g * EPC]), qf[c]);
+        M::run(dpt, ld16(&Vs[(kb * 32 + c32) * SKV + c * KC + g * EPC]), df[c]);
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int key0 = k0 + kb * 32 + 8 * c + 4 * g;
+        f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+        uint32_t mw = 0x01010101u;
+        if (general) {
+          if constexpr (HAS_BIAS) bv = load_bias4(p, p.bias, brow + key0, p.Lk - key0);
+          if (need_mask) mw = load_mask4(p, mrow + key0, p.Lk - key0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * c + j;
+          float x = __builtin_fmaf(s[r], p.scale_log2, neg_lse2);
+          if (general) {
+            const int kk = key0 + j;
+            if constexpr (HAS_BIAS) x = __builtin_fmaf(bv[j], kLog2e, x);
+            bool keep = mask_bit(mw, j) && kk < p.Lk && qok;
+            if (CAUSAL) keep = keep && kk <= qrow;
+            x = keep ? x : -INFINITY;
+          }
+          const float pr = fast_exp2(x);
+          dpt[r] = pr * (dpt[r] - dlt);
+        }
+      }
+#pragma unroll
+      for (int f = 0; f < FPB; ++f) {
+        const Frag pd = M::pack(dpt, f);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          M::run(dq[db], lds_tr_frag(Ks, SKT, kb * 32, db * 32, lane, f), pd);
+      }
+    }
+
+    if (kn < nkt) lstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+    kt = kn;
+  }
+
+  if (qok) {
+    bf16* dqp = (bf16*)p.dq + b * p.q_str[0] + h * p.q_str[1] + (int64_t)qrow * p.q_str[2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d0 = db * 32 + 8 * c + 4 * g;
+        if (d0 < p.D) store4(dqp + d0, dq[db], 4 * c, p.scale);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers.
+// ---------------------------------------------------------------------------
+template <int DP, bool HB, bool CA, int DBM>
+static void launch_dkdv_bf16_t(Params p, hipStream_t stream) {
+  p.nkt = (p.Lk + 127) / 128;
+  const int n = p.B * p.H * p.nkt;
+  hipLaunchKernelGGL((dkdv_bf16_kernel<DP, HB, CA, DBM>), dim3(n), dim3(256), 0,
+                     stream, p);
+}
+
+template <int DP, bool CA>
+static void launch_dkdv_bf16_db(const Params& p, hipStream_t stream) {
+  if (!p.has_bias) {
+    launch_dkdv_bf16_t<DP, false, CA, kDbNone>(p, stream);
+  } else if (p.dbias_mode == kDbiasFull) {
+    launch_dkdv_bf16_t<DP, true, CA, kDbFull>(p, stream);
+  } else if (p.dbias_mode == kDbiasColsum) {
+    launch_dkdv_bf16_t<DP, true, CA, kDbColsum>(p, stream);
+  } else {
+    launch_dkdv_bf16_t<DP, true, CA, kDbNone>(p, stream);
+  }
+}
+
+void launch_dkdv_bf16(const Params& p, int dp, hipStream_t stream) {
+  if (dp == 64) {
+    if (p.causal) launch_dkdv_bf16_db<64, true>(p, stream);
+    else launch_dkdv_bf16_db<64, false>(p, stream);
+  } else {
+    if (p.causal) launch_dkdv_bf16_db<128, true>(p, stream);
+    else launch_dkdv_bf16_db<128, false>(p, stream);
+  }
+}
+
+template <int DP, bool HB, bool CA>
+static void launch_dq_bf16_t(Params p, hipStream_t stream) {
+  p.nqt = (p.Lq + 127) / 128;
+  const int n = p.B * p.H * p.nqt;
+  hipLaunchKernelGGL((dq_bf16_kernel<DP, HB, CA>), dim3(n), dim3(256), 0, stream, p);
+}
+
+template <int DP>
+static void launch_dq_bf16_flags(const Params& p, hipStream_t stream) {
+  if (p.has_bias) {
+    if (p.causal) launch_dq_bf16_t<DP, true, true>(p, stream);
+    else launch_dq_bf16_t<DP, true, false>(p, stream);
+  } else {
+    if (p.causal) launch_dq_bf16_t<DP, false, true>(p, stream);
+    else launch_dq_bf16_t<DP, false, false>(p, stream);
+  }
+}
+
+void launch_dq_bf16(const Params& p, int dp, hipStream_t stream) {
+  if (dp == 64) launch_dq_bf16_flags<64>(p, stream);
+  else launch_dq_bf16_flags<128>(p, stream);
+}
+
+}  // namespace nxa
