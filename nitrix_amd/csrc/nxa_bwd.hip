@@ -15,7 +15,9 @@
 namespace nxa {
 
 // ---------------------------------------------------------------------------
-// delta[b, h, q] = sum_d O[q, d] * dO[q, d]  (fp32).  16 lanes per row.
+// delta[b, h, q] = sum_d O[q, d] * dO[q, d]  (fp32), and lse2 = lse * log2(e)
+// so the backward kernels stream both per-row values straight from memory.
+// 16 lanes per row.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void delta_kernel(const Params p) {
@@ -42,7 +44,10 @@ __global__ __launch_bounds__(256) void delta_kernel(const Params p) {
   acc += __shfl_xor(acc, 4, 16);
   acc += __shfl_xor(acc, 2, 16);
   acc += __shfl_xor(acc, 1, 16);
-  if (row < rows && sub == 0) p.delta[row] = acc;
+  if (row < rows && sub == 0) {
+    p.delta[row] = acc;
+    p.lse2[row] = p.lse[row] * kLog2e;
+  }
 }
 
 // Loads a [ROWS x DP] tile (rows r0.., unit-stride head dim) into a row-major

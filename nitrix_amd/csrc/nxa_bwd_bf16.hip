@@ -11,14 +11,17 @@
 // * streamed tiles stay row-major in LDS; the transposed operands
 //   (dO^T, Q^T for dV/dK, K^T for dQ) come from ds_read_b64_tr_b16, so no
 //   transposed copies are written;
-// * row strides carry a 48-byte pad, conflict-free both for the 16-byte row
-//   reads of the S / dP products and for the transposed reads;
+// * tiles read both ways (Q, dO in dK/dV; K in dQ) are XOR-swizzled by
+//   16-byte chunk, conflict-free for the 16-byte row reads of the S / dP
+//   products and for the transposed reads; row-read-only tiles are padded;
 // * the next tile is fetched into registers while the current one is
 //   consumed (double-buffered LDS, one barrier per tile);
 // * per-row LSE / delta are read as float4 for the four consecutive rows a
 //   lane's accumulator group covers.
 #include "nxa_common.h"
 #include "nxa_launch.h"
+
+#include <type_traits>
 
 namespace nxa {
 
@@ -43,6 +46,11 @@ __device__ __forceinline__ float load_bias1(const Params& p, int64_t off) {
 // dK / dV.  Block = 4 waves x 32 keys (128 keys); streams 64-query tiles.
 // Each wave computes S = Q K^T and dP = dO V^T with the key as the lane's
 // column, so P and dS feed dV^T = dO^T P and dK^T = Q^T dS from registers.
+//
+// Query tiles (Q, dO, lse2, delta) move straight from HBM into a 3-stage LDS
+// ring with direct global->LDS copies, two tiles ahead of the one being
+// consumed; each wave waits only for its own copies of the next tile
+// (vmcnt) before the per-tile barrier.
 // ---------------------------------------------------------------------------
 template <int DP, bool HAS_BIAS, bool CAUSAL, int DBM>
 __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
@@ -50,14 +58,16 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
   using Frag = bf16x8;
   constexpr int EPC = 8, KC = 16;
   constexpr int BNK = 128, BQ = 64;
-  constexpr int SQ = DP + 24;
-  constexpr int TSZ = BQ * SQ;
-  constexpr int NC = DP / KC, NDB = DP / 32, CPR = DP / EPC;
-  constexpr int NCH = BQ * CPR / 256;
+  constexpr int TSZ = BQ * DP;          // swizzled, unpadded tile (elements)
+  constexpr int NC = DP / KC, NDB = DP / 32;
   constexpr int FPB = M::FRAGS_PER_BLOCK;
-  static_assert(NCH >= 1, "tile / block mismatch");
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * 2 * TSZ];
-  __shared__ __attribute__((aligned(16))) float rows[2][2][BQ];
+  constexpr int CPRW = DP / 8;          // 16-byte chunks per row
+  constexpr int RPB = 64 / CPRW;        // rows per 1 KB copy (one wave)
+  constexpr int BPW = TSZ / 512 / 4;    // 1 KB copies per wave per tensor
+  constexpr int LPT = 2 * BPW + 2;      // copies per wave per tile
+  static_assert(BPW >= 1, "tile / block mismatch");
+  __shared__ __attribute__((aligned(16))) bf16 tiles[3][2][TSZ];
+  __shared__ __attribute__((aligned(16))) float rowv[3][4][2][BQ];
   __shared__ uint8_t tcls[kMaxBwdTiles];
 
   const int nblk = p.B * p.H * p.nkt;
@@ -75,7 +85,7 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
 
   const bf16* qp = (const bf16*)p.q + b * p.q_str[0] + h * p.q_str[1];
   const bf16* dop = (const bf16*)p.dout + b * p.o_str[0] + h * p.o_str[1];
-  const float* lsep = p.lse + ((int64_t)b * p.H + h) * p.Lq;
+  const float* lse2p = p.lse2 + ((int64_t)b * p.H + h) * p.Lq;
   const float* dltp = p.delta + ((int64_t)b * p.H + h) * p.Lq;
   const int64_t qs = p.q_str[2], os = p.o_str[2];
 
@@ -92,6 +102,10 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
     for (int t = tid; t < nq; t += 256) tcls[t] = (uint8_t)tclass_g(t);
   __syncthreads();
   auto tclass = [&](int t) -> int { return cls_lds ? tcls[t] : tclass_g(t); };
+  auto next_active = [&](int t) {
+    while (t < nq && !(tclass(t) & 1)) ++t;
+    return t;
+  };
 
   // Stationary K / V fragments (B operands) for this lane's key.
   Frag kf[NC], vf[NC];
@@ -135,86 +149,73 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
           for (int i = 0; i < BQ && t * BQ + i < p.Lq; ++i)
             store_db(p, dbbase + (int64_t)(t * BQ + i) * p.dbias_str[2], 0.f);
   }
+  // The stationary loads complete here, so no wait inside the tile loop has
+  // to cover them (vmcnt there only tracks the tile copies).
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
-  // --- streamed Q / dO tiles ---------------------------------------------------
-  Frag qst[NCH], dst[NCH];
-  float lst = 0.f, dlst = 0.f;
-  auto gload = [&](int q0) {
+  // Copies of query tile t into ring stage st.  Rows past Lq are clamped to
+  // the last row and head-dim chunks past D to chunk 0 (finite values that
+  // the keep-mask or the zero K / V columns cancel).
+  auto issue = [&](int t, int st) {
+    const int q0 = t * BQ;
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int idx = tid + i * 256;
-      const int r = idx / CPR, d = (idx % CPR) * EPC;
-      const int q = q0 + r;
-      const bool ok = q < p.Lq && d < p.D;
-      qst[i] = ok ? ld16(qp + (int64_t)q * qs + d) : zero_frag<bf16>();
-      dst[i] = ok ? ld16(dop + (int64_t)q * os + d) : zero_frag<bf16>();
+    for (int i = 0; i < BPW; ++i) {
+      const int blk = wave * BPW + i;
+      const int row = blk * RPB + lane / CPRW;
+      const int lc = (lane % CPRW) ^ swz<DP>(row);
+      const int q = min(q0 + row, p.Lq - 1);
+      const int col = lc * 8 < p.D ? lc * 8 : 0;
+      dma16(qp + (int64_t)q * qs + col, &tiles[st][0][blk * 512]);
+      dma16(dop + (int64_t)q * os + col, &tiles[st][1][blk * 512]);
     }
-    if (tid < BQ) {
-      const int q = q0 + tid;
-      lst = q < p.Lq ? lsep[q] * kLog2e : 0.f;
-      dlst = q < p.Lq ? dltp[q] : 0.f;
-    }
-  };
-  auto lstore = [&](int buf) {
-    bf16* Qs = smem + buf * 2 * TSZ;
-    bf16* Ds = Qs + TSZ;
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int idx = tid + i * 256;
-      const int r = idx / CPR, d = (idx % CPR) * EPC;
-      *reinterpret_cast<Frag*>(&Qs[r * SQ + d]) = qst[i];
-      *reinterpret_cast<Frag*>(&Ds[r * SQ + d]) = dst[i];
-    }
-    if (tid < BQ) {
-      rows[buf][0][tid] = lst;
-      rows[buf][1][tid] = dlst;
-    }
+    const int q = min(q0 + lane, p.Lq - 1);
+    dma4(lse2p + q, &rowv[st][wave][0][0]);
+    dma4(dltp + q, &rowv[st][wave][1][0]);
   };
 
-  int qt = 0;
-  while (qt < nq && !(tclass(qt) & 1)) ++qt;
-  if (qt < nq) {
-    gload(qt * BQ);
-    lstore(0);
+  int cur = next_active(0);
+  int nxt = cur < nq ? next_active(cur + 1) : nq;
+  if (cur < nq) issue(cur, 0);
+  if (nxt < nq) {
+    issue(nxt, 1);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPT));
+  } else {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   }
-  __syncthreads();
-  int buf = 0;
+  barrier_nofence();
+  int st = 0;
 
-  while (qt < nq) {
-    const int cls = tclass(qt);
-    int qn = qt + 1;
-    while (qn < nq && !(tclass(qn) & 1)) ++qn;
-    if (qn < nq) gload(qn * BQ);
+  while (cur < nq) {
+    const int nxt2 = nxt < nq ? next_active(nxt + 1) : nq;
+    if (nxt2 < nq) issue(nxt2, st == 0 ? 2 : st - 1);
 
-    const bf16* Qs = smem + buf * 2 * TSZ;
-    const bf16* Ds = Qs + TSZ;
-    const float* lse2s = rows[buf][0];
-    const float* dlts = rows[buf][1];
-    const int q0 = qt * BQ;
-
-    f32x16 s[2], dp[2];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[qb][r] = 0.f;
-        dp[qb][r] = 0.f;
-      }
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const int off = (qb * 32 + c32) * SQ + c * KC + g * EPC;
-        M::run(s[qb], ld16(&Qs[off]), kf[c]);
-        M::run(dp[qb], ld16(&Ds[off]), vf[c]);
-      }
+    const int cls = tclass(cur);
+    const bf16* Qs = tiles[st][0];
+    const bf16* Ds = tiles[st][1];
+    const float* lse2s = rowv[st][wave][0];
+    const float* dlts = rowv[st][wave][1];
+    const int q0 = cur * BQ;
 
     const bool need_mask = p.has_mask && !(cls & 2);
     const bool tail = (q0 + BQ > p.Lq) || (kw0 + 32 > p.Lk);
     const bool diag = CAUSAL && (kw0 + 31 > q0);
-    const bool general = need_mask || tail || diag || bias_rows;
+
+    // One 32-query block: S, dP -> P, dS -> dV, dK updates.  GEN selects the
+    // masked / per-row-bias body; the fast body is straight-line code.
+    auto block = [&](int qb, auto gen_tag) {
+      constexpr bool GEN = decltype(gen_tag)::value;
+      f32x16 s, dp;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+      for (int r = 0; r < 16; ++r) {
+        s[r] = 0.f;
+        dp[r] = 0.f;
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int off = swz_off<DP>(qb * 32 + c32, 2 * c + g);
+        M::run(s, ld16(&Qs[off]), kf[c]);
+        M::run(dp, ld16(&Ds[off]), vf[c]);
+      }
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int ql0 = qb * 32 + 8 * c + 4 * g;
@@ -223,9 +224,9 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 4 * c + j;
-          float x = __builtin_fmaf(s[qb][r], p.scale_log2, -l4[j]);
+          float x = __builtin_fmaf(s[r], p.scale_log2, -l4[j]);
           if constexpr (HAS_BIAS) x += bkey;
-          if (general) {
+          if constexpr (GEN) {
             const int q = q0 + ql0 + j;
             const int qcl = q < p.Lq ? q : p.Lq - 1;
             if constexpr (HAS_BIAS)
@@ -238,9 +239,9 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
             x = keep ? x : -INFINITY;
           }
           const float pr = fast_exp2(x);
-          const float ds = pr * (dp[qb][r] - d4[j]);
-          s[qb][r] = pr;
-          dp[qb][r] = ds;
+          const float ds = pr * (dp[r] - d4[j]);
+          s[r] = pr;
+          dp[r] = ds;
           if constexpr (DBM == kDbFull) {
             const int q = q0 + ql0 + j;
             if (kok && q < p.Lq) store_db(p, dbbase + (int64_t)q * p.dbias_str[2], ds);
@@ -248,25 +249,35 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
           if constexpr (DBM == kDbColsum) colsum += ds;
         }
       }
-
-    // dV^T += dO^T P, dK^T += Q^T dS (transposed operands via ds_read_tr).
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+      // dV^T += dO^T P, dK^T += Q^T dS (transposed operands via ds_read_tr).
 #pragma unroll
       for (int f = 0; f < FPB; ++f) {
-        const Frag pp = M::pack(s[qb], f);
-        const Frag pd = M::pack(dp[qb], f);
+        const Frag pp = M::pack(s, f);
+        const Frag pd = M::pack(dp, f);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          M::run(dv[db], lds_tr_frag(Ds, SQ, qb * 32, db * 32, lane, f), pp);
-          M::run(dk[db], lds_tr_frag(Qs, SQ, qb * 32, db * 32, lane, f), pd);
+          M::run(dv[db], lds_tr_frag_swz<DP>(Ds, qb * 32, db * 32, lane, f), pp);
+          M::run(dk[db], lds_tr_frag_swz<DP>(Qs, qb * 32, db * 32, lane, f), pd);
         }
       }
+    };
+    if (need_mask || tail || diag || bias_rows) {
+      block(0, std::true_type{});
+      block(1, std::true_type{});
+    } else {
+      block(0, std::false_type{});
+      block(1, std::false_type{});
+    }
 
-    if (qn < nq) lstore(buf ^ 1);
-    __syncthreads();
-    buf ^= 1;
-    qt = qn;
+    // Tile nxt must be resident before the barrier; nxt2 may stay in flight.
+    if (nxt2 < nq)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPT));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    barrier_nofence();
+    st = st == 2 ? 0 : st + 1;
+    cur = nxt;
+    nxt = nxt2;
   }
 
   if (kok) {
@@ -293,7 +304,9 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
 // dQ.  Block = 4 waves x 32 queries (128); streams 64-key tiles in two
 // 32-key halves.  S^T = K Q^T and dP^T = V dO^T put the query on the lane's
 // column, so dS^T feeds dQ^T = K^T dS^T from registers; K^T is read
-// transposed from the row-major K tile.
+// transposed from the row-major K tile.  K / V tiles arrive by direct
+// global->LDS copies into a double-buffered ring (no staging registers), one
+// tile ahead; two blocks share a CU.
 // ---------------------------------------------------------------------------
 template <int DP, bool HAS_BIAS, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
@@ -301,13 +314,13 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
   using Frag = bf16x8;
   constexpr int EPC = 8, KC = 16;
   constexpr int BM = 128, BN = 64;
-  constexpr int SKT = DP + 24;  // K: row reads and transposed reads
-  constexpr int SKV = DP + 8;   // V: row reads only
-  constexpr int KSZ = BN * SKT, VSZ = BN * SKV;
-  constexpr int NC = DP / KC, NDB = DP / 32, CPR = DP / EPC;
-  constexpr int NCH = BN * CPR / 256;
+  constexpr int TSZ = BN * DP;         // swizzled, unpadded tile (elements)
+  constexpr int NC = DP / KC, NDB = DP / 32;
   constexpr int FPB = M::FRAGS_PER_BLOCK;
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * (KSZ + VSZ)];
+  constexpr int CPRW = DP / 8;
+  constexpr int RPB = 64 / CPRW;
+  constexpr int BPW = TSZ / 512 / 4;
+  __shared__ __attribute__((aligned(16))) bf16 tiles[2][2][TSZ];  // [stage][K|V]
   __shared__ uint8_t tcls[kMaxBwdTiles];
 
   const int nblk = p.B * p.H * p.nqt;
@@ -339,6 +352,10 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
     if (cls_lds) return tcls[t];
     return tile_class(p, b, h, q0, q0 + BM, t * BN, t * BN + BN);
   };
+  auto next_active = [&](int t) {
+    while (t < nkt && !(tclass(t) & 1)) ++t;
+    return t;
+  };
 
   Frag qf[NC], df[NC];
   {
@@ -355,7 +372,7 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
     }
   }
   const int64_t rowid = ((int64_t)b * p.H + h) * p.Lq + qc;
-  const float neg_lse2 = -p.lse[rowid] * kLog2e;
+  const float neg_lse2 = -p.lse2[rowid];
   const float dlt = p.delta[rowid];
   const int64_t brow = HAS_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] +
                                       (int64_t)qc * p.bias_str[2]
@@ -364,6 +381,9 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
                                          h * p.mask_str[1] +
                                          (int64_t)qc * p.mask_str[2]
                                    : nullptr;
+  // Stationary loads complete before the copies start (vmcnt in the loop
+  // then only tracks tile copies).
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   f32x16 dq[NDB];
 #pragma unroll
@@ -371,53 +391,41 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
 
-  Frag kst[NCH], vst[NCH];
-  auto gload = [&](int k0) {
+  // Copies of key tile t into ring stage st (rows past Lk clamped to the last
+  // key, head-dim chunks past D to chunk 0; both are masked or cancelled).
+  auto issue = [&](int t, int st) {
+    const int k0 = t * BN;
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int idx = tid + i * 256;
-      const int r = idx / CPR, d = (idx % CPR) * EPC;
-      const int key = k0 + r;
-      const bool ok = key < p.Lk && d < p.D;
-      kst[i] = ok ? ld16(kp + (int64_t)key * ks + d) : zero_frag<bf16>();
-      vst[i] = ok ? ld16(vp + (int64_t)key * vs + d) : zero_frag<bf16>();
-    }
-  };
-  auto lstore = [&](int buf) {
-    bf16* Ks = smem + buf * (KSZ + VSZ);
-    bf16* Vs = Ks + KSZ;
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int idx = tid + i * 256;
-      const int r = idx / CPR, d = (idx % CPR) * EPC;
-      *reinterpret_cast<Frag*>(&Ks[r * SKT + d]) = kst[i];
-      *reinterpret_cast<Frag*>(&Vs[r * SKV + d]) = vst[i];
+    for (int i = 0; i < BPW; ++i) {
+      const int blk = wave * BPW + i;
+      const int row = blk * RPB + lane / CPRW;
+      const int lc = (lane % CPRW) ^ swz<DP>(row);
+      const int key = min(k0 + row, p.Lk - 1);
+      const int col = lc * 8 < p.D ? lc * 8 : 0;
+      dma16(kp + (int64_t)key * ks + col, &tiles[st][0][blk * 512]);
+      dma16(vp + (int64_t)key * vs + col, &tiles[st][1][blk * 512]);
     }
   };
 
-  int kt = 0;
-  while (kt < nkt && !(tclass(kt) & 1)) ++kt;
-  if (kt < nkt) {
-    gload(kt * BN);
-    lstore(0);
-  }
-  __syncthreads();
-  int buf = 0;
+  int kt = next_active(0);
+  if (kt < nkt) issue(kt, 0);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  barrier_nofence();
+  int st = 0;
 
   while (kt < nkt) {
     const int cls = tclass(kt);
-    int kn = kt + 1;
-    while (kn < nkt && !(tclass(kn) & 1)) ++kn;
-    if (kn < nkt) gload(kn * BN);
+    const int kn = next_active(kt + 1);
+    if (kn < nkt) issue(kn, st ^ 1);
 
-    const bf16* Ks = smem + buf * (KSZ + VSZ);
-    const bf16* Vs = Ks + KSZ;
+    const bf16* Ks = tiles[st][0];
+    const bf16* Vs = tiles[st][1];
     const int k0 = kt * BN;
     const bool need_mask = p.has_mask && !(cls & 2);
     const bool tail = k0 + BN > p.Lk;
     const bool diag = CAUSAL && (k0 + BN - 1 > qw0);
-    const bool general = HAS_BIAS || need_mask || tail || diag;
 
+    const bool general = HAS_BIAS || need_mask || tail || diag;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       f32x16 s, dpt;
@@ -428,8 +436,9 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
       }
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        M::run(s, ld16(&Ks[(kb * 32 + c32) * SKT + c * KC + g * EPC]), qf[c]);
-        M::run(dpt, ld16(&Vs[(kb * 32 + c32) * SKV + c * KC + g * EPC]), df[c]);
+        const int off = swz_off<DP>(kb * 32 + c32, 2 * c + g);
+        M::run(s, ld16(&Ks[off]), qf[c]);
+        M::run(dpt, ld16(&Vs[off]), df[c]);
       }
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -460,13 +469,13 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
         const Frag pd = M::pack(dpt, f);
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
-          M::run(dq[db], lds_tr_frag(Ks, SKT, kb * 32, db * 32, lane, f), pd);
+          M::run(dq[db], lds_tr_frag_swz<DP>(Ks, kb * 32, db * 32, lane, f), pd);
       }
     }
 
-    if (kn < nkt) lstore(buf ^ 1);
-    __syncthreads();
-    buf ^= 1;
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // tile kn resident
+    barrier_nofence();
+    st ^= 1;
     kt = kn;
   }
 

@@ -59,7 +59,8 @@ struct Params {
   void* dk;
   void* dv;
   void* dbias;         // final dbias, or the fp32 partial buffer (dbias_f32=1)
-  float* delta;
+  float* delta;        // [B, H, Lq] rowsum(O * dO)        (backward workspace)
+  float* lse2;         // [B, H, Lq] lse * log2(e)          (backward workspace)
   const uint8_t* tilemap;
   uint8_t* tilemap_out;
 
@@ -198,6 +199,74 @@ __device__ __forceinline__ bf16x8 lds_tr_frag(const bf16* tile, int stride,
   typedef short i16x8 __attribute__((ext_vector_type(8)));
   const i16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return __builtin_bit_cast(bf16x8, r);
+}
+
+// XOR-swizzled bf16 tiles with DP columns and no row padding.  The 16-byte
+// chunk c of row r is stored at chunk c ^ swz(r).  The swizzle is
+// conflict-free (64 banks x 4 bytes) both for 16-byte row reads of 16
+// consecutive rows and for ds_read_b64_tr_b16 reads, whose 32 lanes cover
+// 4 consecutive rows x 64 bytes; plain padding cannot serve both patterns.
+template <int DP>
+__device__ __forceinline__ int swz(int r);
+template <>
+__device__ __forceinline__ int swz<128>(int r) {
+  return 4 * (r & 3) + ((r >> 2) & 3);
+}
+template <>
+__device__ __forceinline__ int swz<64>(int r) {
+  return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
+}
+template <int DP>
+__device__ __forceinline__ int swz_off(int row, int chunk) {
+  return row * DP + 8 * (chunk ^ swz<DP>(row));
+}
+
+// lds_tr_frag for a swizzled tile (see lds_tr_frag for the lane mapping).
+template <int DP>
+__device__ __forceinline__ bf16x8 lds_tr_frag_swz(const bf16* tile, int r0,
+                                                  int col0, int lane, int f) {
+  const int grp = lane >> 4, i = lane & 15;
+  const int row = r0 + 16 * f + 4 * (grp >> 1) + (i >> 2);
+  const int col = col0 + 16 * (grp & 1) + 4 * (i & 3);
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const bf16* p0 = tile + swz_off<DP>(row, col >> 3) + (col & 7);
+  const bf16* p1 = tile + swz_off<DP>(row + 8, col >> 3) + (col & 7);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p1);
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  const i16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// ---------------------------------------------------------------------------
+// Direct global -> LDS copies (no staging registers).  For one wave, lane l's
+// `size` bytes land at lds + l * size; the LDS address must be wave-uniform.
+// Completion is tracked by vmcnt like any vector load.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(
+      g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(
+      g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+
+// s_waitcnt immediate that waits for vmcnt <= n and leaves expcnt / lgkmcnt
+// unconstrained (gfx9 encoding: vmcnt bits [3:0] and [15:14]).
+__device__ __forceinline__ constexpr int vmcnt_imm(int n) {
+  return (n & 0xF) | (((n >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8);
+}
+
+// Workgroup barrier without a memory fence: LDS filled by direct copies is
+// published by each wave's own vmcnt wait before the barrier (a fenced
+// __syncthreads would wait for every copy still in flight, including the
+// prefetch of later tiles).  The empty asm statements keep the compiler from
+// moving memory accesses across the barrier.
+__device__ __forceinline__ void barrier_nofence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
