@@ -100,6 +100,14 @@ def main() -> int:
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=5)
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument(
+        '--copy-calibration',
+        type=int,
+        default=0,
+        metavar='MIB',
+        help='only run 5 device-to-device copies of MIB MiB (reference '
+        'kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)',
+    )
     args = ap.parse_args()
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
@@ -112,6 +120,16 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device='cuda:0').fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({'copy_calibration_bytes_per_copy': n}), flush=True)
+        return 0
 
     from nitrix_amd import _lib, scaled_dot_product_attention
 

@@ -1,0 +1,158 @@
+"""The C ABI of ``libnxattn.so`` on the CPU (no GPU needed).
+
+* the library loads and exports every function ``include/nxattn.h`` declares;
+* host-side descriptor validation (the counterpart of the reference's
+  ``_check_tileable``, ``src/nitrix/_kernels/cuda/attention.py:708-765``)
+  returns the documented error codes and a message;
+* the workspace sizes follow the documented layout;
+* entry points reject NULL / misaligned buffers before touching the GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from nitrix_amd import _lib
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / 'include' / 'nxattn.h'
+
+
+@pytest.fixture(scope='module')
+def lib():
+    if not _lib.LIB_PATH.exists():
+        from nitrix_amd import _build
+
+        _build.build()
+    return _lib.lib()
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    # drop comments
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(nxa_[a-z_]+)\s*\(', text)))
+
+
+def test_header_declares_the_expected_api():
+    assert _declared_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_function(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.nxa_version() == 1
+
+
+def _desc(B=2, H=3, Lq=100, Lk=70, D=64, dtype=_lib.NXA_BF16):
+    d = _lib.NxaDesc()
+    d.B, d.H, d.Lq, d.Lk, d.D = B, H, Lq, Lk, D
+    d.io_dtype = dtype
+    d.bias_dtype = dtype
+    d.scale = 0.125
+    d.q_str[:] = (H * Lq * D, Lq * D, D)
+    d.k_str[:] = (H * Lk * D, Lk * D, D)
+    d.v_str[:] = (H * Lk * D, Lk * D, D)
+    d.o_str[:] = (H * Lq * D, Lq * D, D)
+    d.bias_str[:] = (0, Lq * Lk, Lk)
+    d.mask_str[:] = (Lk, 0, 0)
+    return d
+
+
+def _check(lib, d, has_bias=1, has_mask=1):
+    return lib.nxa_check(ctypes.byref(d), has_bias, has_mask)
+
+
+def test_valid_descriptor(lib):
+    assert _check(lib, _desc()) == _lib.NXA_OK
+    assert _check(lib, _desc(dtype=_lib.NXA_F32, D=12)) == _lib.NXA_OK
+
+
+@pytest.mark.parametrize(
+    'mutate, code, text',
+    [
+        (lambda d: setattr(d, 'io_dtype', 7), _lib.NXA_E_DTYPE, 'io_dtype'),
+        (lambda d: setattr(d, 'bias_dtype', 9), _lib.NXA_E_DTYPE, 'bias_dtype'),
+        (lambda d: setattr(d, 'Lq', 0), _lib.NXA_E_SHAPE, 'positive'),
+        (lambda d: setattr(d, 'D', 136), _lib.NXA_E_UNSUPPORTED, 'exceeds 128'),
+        (lambda d: setattr(d, 'D', 12), _lib.NXA_E_UNSUPPORTED, 'multiple of 8'),
+        (lambda d: d.q_str.__setitem__(2, 65), _lib.NXA_E_LAYOUT, 'stride'),
+        (lambda d: d.k_str.__setitem__(0, -64), _lib.NXA_E_LAYOUT, 'negative'),
+        (lambda d: d.bias_str.__setitem__(1, -1), _lib.NXA_E_LAYOUT, 'bias'),
+    ],
+)
+def test_invalid_descriptors(lib, mutate, code, text):
+    d = _desc()
+    mutate(d)
+    assert _check(lib, d) == code
+    assert text in lib.nxa_last_error().decode()
+
+
+def test_null_descriptor(lib):
+    assert lib.nxa_check(None, 0, 0) == _lib.NXA_E_ARG
+
+
+def test_workspace_layout(lib):
+    d = _desc(B=2, H=3, Lq=100, Lk=70)
+    # no mask, no bias: the forward needs nothing
+    assert lib.nxa_workspace_bytes(ctypes.byref(d), 0, 0, 0) == 0
+    # mask [B,1,1,Lk] (zero H / Lq strides): one row of 64-key tiles per batch
+    mb = 2 * 1 * 1 * 2  # MB * MH * MQ * MK
+    assert lib.nxa_workspace_bytes(ctypes.byref(d), 0, 1, 0) == 256 * (
+        (mb + 255) // 256
+    )
+    # backward: delta and lse2 rows (2 x B*H*Lq fp32), 256-byte aligned each
+    rows = 2 * 3 * 100 * 4
+    assert lib.nxa_workspace_bytes(ctypes.byref(d), 0, 0, 1) == 2 * 256 * (
+        (rows + 255) // 256
+    )
+    # bias shared over the batch: fp32 dbias partials [B,H,Lq,Lk] are added
+    part = 2 * 3 * 100 * 70 * 4
+    got = lib.nxa_workspace_bytes(ctypes.byref(d), 1, 0, 1)
+    assert got == 2 * 256 * ((rows + 255) // 256) + 256 * ((part + 255) // 256)
+
+
+def test_entry_points_reject_null_buffers_without_a_gpu(lib):
+    d = _desc()
+    rc = lib.nxa_fwd(ctypes.byref(d), None, None, None, None, None, None, None,
+                     None, 0, None)
+    assert rc == _lib.NXA_E_ARG
+    assert 'NULL' in lib.nxa_last_error().decode()
+    rc = lib.nxa_bwd(ctypes.byref(d), None, None, None, None, None, None, None,
+                     None, None, None, None, None, None, None, 0, 0, None)
+    assert rc == _lib.NXA_E_ARG
+
+
+def test_entry_points_reject_misaligned_buffers(lib):
+    d = _desc()
+    odd = ctypes.c_void_p(0x1008)
+    ok = ctypes.c_void_p(0x2000)
+    rc = lib.nxa_fwd(ctypes.byref(d), odd, ok, ok, None, None, ok, None, None,
+                     0, None)
+    assert rc == _lib.NXA_E_LAYOUT
+    assert '16-byte' in lib.nxa_last_error().decode()
+
+
+def test_forward_with_mask_requires_workspace(lib):
+    d = _desc()
+    ok = ctypes.c_void_p(0x2000)
+    rc = lib.nxa_fwd(ctypes.byref(d), ok, ok, ok, None, ok, ok, None, None, 0,
+                     None)
+    assert rc == _lib.NXA_E_WORKSPACE
+
+
+def test_backward_rejects_broadcast_keys(lib):
+    d = _desc()
+    d.k_str[1] = 0  # k shared over heads
+    ok = ctypes.c_void_p(0x2000)
+    rc = lib.nxa_bwd(ctypes.byref(d), ok, ok, ok, None, None, ok, ok, ok, ok,
+                     ok, ok, None, None, ok, 1 << 20, 0, None)
+    assert rc == _lib.NXA_E_UNSUPPORTED
+
+
+def test_profile_read_without_records(lib):
+    _lib.profile_reset()
+    assert _lib.profile_read('fwd') == (0.0, 0)
