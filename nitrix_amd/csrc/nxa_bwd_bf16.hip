@@ -43,31 +43,33 @@ __device__ __forceinline__ float load_bias1(const Params& p, int64_t off) {
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV.  Block = 4 waves x 32 keys (128 keys); streams 64-query tiles.
-// Each wave computes S = Q K^T and dP = dO V^T with the key as the lane's
-// column, so P and dS feed dV^T = dO^T P and dK^T = Q^T dS from registers.
+// dK / dV.  Block = 8 waves over 128 keys: waves 0-3 accumulate dV, waves 4-7
+// accumulate dK (and dbias) for the same 32-key column each; a dV wave and a
+// dK wave share a SIMD, so one's softmax VALU overlaps the other's MFMAs.
+// Splitting the roles keeps each wave under 256 registers (two waves per
+// SIMD) at the price of computing S = Q K^T in both roles.
 //
-// Query tiles (Q, dO, lse2, delta) move straight from HBM into a 3-stage LDS
-// ring with direct global->LDS copies, two tiles ahead of the one being
-// consumed; each wave waits only for its own copies of the next tile
-// (vmcnt) before the per-tile barrier.
+// Each wave computes S = Q K^T (and dP = dO V^T for dK) with the key as the
+// lane's column, so P and dS feed dV^T = dO^T P and dK^T = Q^T dS from
+// registers.  Query tiles (Q, dO, lse2, delta) move straight from HBM into a
+// 3-stage LDS ring with direct global->LDS copies, two tiles ahead; each wave
+// waits only for its own copies of the next tile before the per-tile barrier.
 // ---------------------------------------------------------------------------
 template <int DP, bool HAS_BIAS, bool CAUSAL, int DBM>
-__global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
+__global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
   using M = Mma<bf16>;
   using Frag = bf16x8;
   constexpr int EPC = 8, KC = 16;
-  constexpr int BNK = 128, BQ = 64;
-  constexpr int TSZ = BQ * DP;          // swizzled, unpadded tile (elements)
+  constexpr int BNK = 128, BQ = 64, NW = 8;
+  using PT = PTile<DP>;
+  using PC = PTileCopy<DP, NW>;
   constexpr int NC = DP / KC, NDB = DP / 32;
   constexpr int FPB = M::FRAGS_PER_BLOCK;
-  constexpr int CPRW = DP / 8;          // 16-byte chunks per row
-  constexpr int RPB = 64 / CPRW;        // rows per 1 KB copy (one wave)
-  constexpr int BPW = TSZ / 512 / 4;    // 1 KB copies per wave per tensor
-  constexpr int LPT = 2 * BPW + 2;      // copies per wave per tile
-  static_assert(BPW >= 1, "tile / block mismatch");
-  __shared__ __attribute__((aligned(16))) bf16 tiles[3][2][TSZ];
-  __shared__ __attribute__((aligned(16))) float rowv[3][4][2][BQ];
+  // copies per wave per query tile (Q, dO, lse2, delta)
+  constexpr int LPT_HI = 2 * PC::CNT_HI + 2, LPT_LO = 2 * PC::CNT_LO + 2;
+  static_assert(PT::ROWS == BQ, "tile / block mismatch");
+  __shared__ __attribute__((aligned(16))) bf16 tiles[3][2][PT::ELEMS];
+  __shared__ __attribute__((aligned(16))) float rowv[3][NW][2][BQ];
   __shared__ uint8_t tcls[kMaxBwdTiles];
 
   const int nblk = p.B * p.H * p.nkt;
@@ -76,9 +78,10 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
   const int kt = vid % p.nkt;
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool is_dk = wave >= 4;  // wave-uniform role
   const int g = lane >> 5, c32 = lane & 31;
   const int kblk0 = kt * BNK;
-  const int kw0 = kblk0 + wave * 32;
+  const int kw0 = kblk0 + (wave & 3) * 32;
   const int key = kw0 + c32;
   const bool kok = key < p.Lk;
   const int kc = kok ? key : p.Lk - 1;
@@ -99,7 +102,7 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
     return tile_class(p, b, h, q0, q0 + BQ, kblk0, kblk0 + BNK);
   };
   if (cls_lds)
-    for (int t = tid; t < nq; t += 256) tcls[t] = (uint8_t)tclass_g(t);
+    for (int t = tid; t < nq; t += NW * 64) tcls[t] = (uint8_t)tclass_g(t);
   __syncthreads();
   auto tclass = [&](int t) -> int { return cls_lds ? tcls[t] : tclass_g(t); };
   auto next_active = [&](int t) {
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
     return t;
   };
 
-  // Stationary K / V fragments (B operands) for this lane's key.
+  // Stationary B operands: K (both roles), V (dK role) for this lane's key.
   Frag kf[NC], vf[NC];
   {
     const bf16* kp = (const bf16*)p.k + b * p.k_str[0] + h * p.k_str[1] +
@@ -119,17 +122,14 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
       const int d = c * KC + g * EPC;
       const bool ok = kok && d < p.D;
       kf[c] = ok ? ld16(kp + d) : zero_frag<bf16>();
-      vf[c] = ok ? ld16(vp + d) : zero_frag<bf16>();
+      vf[c] = (ok && is_dk) ? ld16(vp + d) : zero_frag<bf16>();
     }
   }
-  f32x16 dk[NDB], dv[NDB];
+  f32x16 acc[NDB];  // dV^T (dV role) or dK^T (dK role)
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      dk[db][r] = 0.f;
-      dv[db][r] = 0.f;
-    }
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
   float colsum = 0.f;
 
   // Bias: a per-key constant when it broadcasts over queries, else per row.
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
 
   // Full dbias: entries of skipped tiles are zero.
   if constexpr (DBM == kDbFull) {
-    if (kok)
+    if (is_dk && kok)
       for (int t = 0; t < nq; ++t)
         if (!(tclass(t) & 1))
           for (int i = 0; i < BQ && t * BQ + i < p.Lq; ++i)
@@ -158,145 +158,164 @@ __global__ __launch_bounds__(256) void dkdv_bf16_kernel(const Params p) {
   // the keep-mask or the zero K / V columns cancel).
   auto issue = [&](int t, int st) {
     const int q0 = t * BQ;
-#pragma unroll
-    for (int i = 0; i < BPW; ++i) {
-      const int blk = wave * BPW + i;
-      const int row = blk * RPB + lane / CPRW;
-      const int lc = (lane % CPRW) ^ swz<DP>(row);
-      const int q = min(q0 + row, p.Lq - 1);
-      const int col = lc * 8 < p.D ? lc * 8 : 0;
-      dma16(qp + (int64_t)q * qs + col, &tiles[st][0][blk * 512]);
-      dma16(dop + (int64_t)q * os + col, &tiles[st][1][blk * 512]);
-    }
+    PC::issue(qp, qs, q0, p.Lq, p.D, &tiles[st][0][0], wave, lane);
+    PC::issue(dop, os, q0, p.Lq, p.D, &tiles[st][1][0], wave, lane);
     const int q = min(q0 + lane, p.Lq - 1);
     dma4(lse2p + q, &rowv[st][wave][0][0]);
     dma4(dltp + q, &rowv[st][wave][1][0]);
   };
-
-  int cur = next_active(0);
-  int nxt = cur < nq ? next_active(cur + 1) : nq;
-  if (cur < nq) issue(cur, 0);
-  if (nxt < nq) {
-    issue(nxt, 1);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPT));
-  } else {
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-  }
-  barrier_nofence();
-  int st = 0;
-
-  while (cur < nq) {
-    const int nxt2 = nxt < nq ? next_active(nxt + 1) : nq;
-    if (nxt2 < nq) issue(nxt2, st == 0 ? 2 : st - 1);
-
-    const int cls = tclass(cur);
-    const bf16* Qs = tiles[st][0];
-    const bf16* Ds = tiles[st][1];
-    const float* lse2s = rowv[st][wave][0];
-    const float* dlts = rowv[st][wave][1];
-    const int q0 = cur * BQ;
-
-    const bool need_mask = p.has_mask && !(cls & 2);
-    const bool tail = (q0 + BQ > p.Lq) || (kw0 + 32 > p.Lk);
-    const bool diag = CAUSAL && (kw0 + 31 > q0);
-
-    // One 32-query block: S, dP -> P, dS -> dV, dK updates.  GEN selects the
-    // masked / per-row-bias body; the fast body is straight-line code.
-    auto block = [&](int qb, auto gen_tag) {
-      constexpr bool GEN = decltype(gen_tag)::value;
-      f32x16 s, dp;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = 0.f;
-        dp[r] = 0.f;
-      }
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int off = swz_off<DP>(qb * 32 + c32, 2 * c + g);
-        M::run(s, ld16(&Qs[off]), kf[c]);
-        M::run(dp, ld16(&Ds[off]), vf[c]);
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int ql0 = qb * 32 + 8 * c + 4 * g;
-        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&lse2s[ql0]);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dlts[ql0]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = 4 * c + j;
-          float x = __builtin_fmaf(s[r], p.scale_log2, -l4[j]);
-          if constexpr (HAS_BIAS) x += bkey;
-          if constexpr (GEN) {
-            const int q = q0 + ql0 + j;
-            const int qcl = q < p.Lq ? q : p.Lq - 1;
-            if constexpr (HAS_BIAS)
-              if (bias_rows)
-                x = __builtin_fmaf(
-                    load_bias1(p, bbase + (int64_t)qcl * p.bias_str[2]), kLog2e, x);
-            bool keep = q < p.Lq && kok;
-            if (need_mask) keep = keep && mbase[(int64_t)qcl * p.mask_str[2]] != 0;
-            if (CAUSAL) keep = keep && key <= q;
-            x = keep ? x : -INFINITY;
-          }
-          const float pr = fast_exp2(x);
-          const float ds = pr * (dp[r] - d4[j]);
-          s[r] = pr;
-          dp[r] = ds;
-          if constexpr (DBM == kDbFull) {
-            const int q = q0 + ql0 + j;
-            if (kok && q < p.Lq) store_db(p, dbbase + (int64_t)q * p.dbias_str[2], ds);
-          }
-          if constexpr (DBM == kDbColsum) colsum += ds;
-        }
-      }
-      // dV^T += dO^T P, dK^T += Q^T dS (transposed operands via ds_read_tr).
-#pragma unroll
-      for (int f = 0; f < FPB; ++f) {
-        const Frag pp = M::pack(s, f);
-        const Frag pd = M::pack(dp, f);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          M::run(dv[db], lds_tr_frag_swz<DP>(Ds, qb * 32, db * 32, lane, f), pp);
-          M::run(dk[db], lds_tr_frag_swz<DP>(Qs, qb * 32, db * 32, lane, f), pd);
-        }
-      }
-    };
-    if (need_mask || tail || diag || bias_rows) {
-      block(0, std::true_type{});
-      block(1, std::true_type{});
-    } else {
-      block(0, std::false_type{});
-      block(1, std::false_type{});
-    }
-
-    // Tile nxt must be resident before the barrier; nxt2 may stay in flight.
-    if (nxt2 < nq)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPT));
-    else
+  // Waits until the tile issued before the most recent one is resident
+  // (more = a later tile is still in flight) or until everything is.
+  auto wait_tiles = [&](bool more) {
+    if (!more)
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    else if (wave < PC::N_HI)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPT_HI));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPT_LO));
+  };
+
+  // The tile loop is instantiated per role (dV / dK): identical barrier
+  // sequence, role-specific straight-line bodies.
+  auto run = [&](auto role_tag) {
+    constexpr bool DK = decltype(role_tag)::value;
+    int cur = next_active(0);
+    int nxt = cur < nq ? next_active(cur + 1) : nq;
+    if (cur < nq) issue(cur, 0);
+    if (nxt < nq) issue(nxt, 1);
+    wait_tiles(nxt < nq);
     barrier_nofence();
-    st = st == 2 ? 0 : st + 1;
-    cur = nxt;
-    nxt = nxt2;
-  }
+    int st = 0;
+
+    while (cur < nq) {
+      const int nxt2 = nxt < nq ? next_active(nxt + 1) : nq;
+      if (nxt2 < nq) issue(nxt2, st == 0 ? 2 : st - 1);
+
+      const int cls = tclass(cur);
+      const bf16* Qs = tiles[st][0];
+      const bf16* Ds = tiles[st][1];
+      const float* lse2s = rowv[st][wave][0];
+      const float* dlts = rowv[st][wave][1];
+      const int q0 = cur * BQ;
+      const bool need_mask = p.has_mask && !(cls & 2);
+      const bool tail = (q0 + BQ > p.Lq) || (kw0 + 32 > p.Lk);
+      const bool diag = CAUSAL && (kw0 + 31 > q0);
+      const bool general = need_mask || tail || diag || bias_rows;
+
+      // One 32-query block; GEN selects the masked / per-row-bias body so the
+      // interior-tile body is straight-line code.
+      auto block = [&](int qb, auto gen_tag) {
+        constexpr bool GEN = decltype(gen_tag)::value;
+        // S = Q K^T (both roles); dP = dO V^T (dK role).
+        f32x16 s, dp;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          s[r] = 0.f;
+          dp[r] = 0.f;
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int off = PT::row_off(qb * 32 + c32, c * KC + g * EPC);
+          M::run(s, ld16(&Qs[off]), kf[c]);
+          if constexpr (DK) M::run(dp, ld16(&Ds[off]), vf[c]);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int ql0 = qb * 32 + 8 * c + 4 * g;
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&lse2s[ql0]);
+          f32x4 d4 = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (DK) d4 = *reinterpret_cast<const f32x4*>(&dlts[ql0]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * c + j;
+            float x = __builtin_fmaf(s[r], p.scale_log2, -l4[j]);
+            if constexpr (HAS_BIAS) x += bkey;
+            if constexpr (GEN) {
+              const int q = q0 + ql0 + j;
+              const int qcl = q < p.Lq ? q : p.Lq - 1;
+              if constexpr (HAS_BIAS)
+                if (bias_rows)
+                  x = __builtin_fmaf(
+                      load_bias1(p, bbase + (int64_t)qcl * p.bias_str[2]), kLog2e, x);
+              bool keep = q < p.Lq && kok;
+              if (need_mask) keep = keep && mbase[(int64_t)qcl * p.mask_str[2]] != 0;
+              if (CAUSAL) keep = keep && key <= q;
+              x = keep ? x : -INFINITY;
+            }
+            const float pr = fast_exp2(x);
+            if constexpr (DK) {
+              const float ds = pr * (dp[r] - d4[j]);
+              s[r] = ds;
+              if constexpr (DBM == kDbFull) {
+                const int q = q0 + ql0 + j;
+                if (kok && q < p.Lq)
+                  store_db(p, dbbase + (int64_t)q * p.dbias_str[2], ds);
+              }
+              if constexpr (DBM == kDbColsum) colsum += ds;
+            } else {
+              s[r] = pr;
+            }
+          }
+        }
+        // dV^T += dO^T P (dV role) or dK^T += Q^T dS (dK role).
+        const bf16* At = DK ? Qs : Ds;
+#pragma unroll
+        for (int f = 0; f < FPB; ++f) {
+          const Frag pf = M::pack(s, f);
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+            M::run(acc[db], ptile_tr_frag<DP>(At, qb * 32, db * 32, lane, f), pf);
+        }
+      };
+      // The scheduling barrier keeps block 1's loads from being hoisted into
+      // block 0, which would exceed the two-waves-per-SIMD register budget.
+      if (general) {
+        block(0, std::true_type{});
+        __builtin_amdgcn_sched_barrier(0);
+        block(1, std::true_type{});
+      } else {
+        block(0, std::false_type{});
+        __builtin_amdgcn_sched_barrier(0);
+        block(1, std::false_type{});
+      }
+
+      // Tile nxt must be resident before the barrier; nxt2 may stay in flight.
+      wait_tiles(nxt2 < nq);
+      barrier_nofence();
+      st = st == 2 ? 0 : st + 1;
+      cur = nxt;
+      nxt = nxt2;
+    }
+  };
+  if (is_dk)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
 
   if (kok) {
-    bf16* dkp = (bf16*)p.dk + b * p.k_str[0] + h * p.k_str[1] + (int64_t)key * p.k_str[2];
-    bf16* dvp = (bf16*)p.dv + b * p.v_str[0] + h * p.v_str[1] + (int64_t)key * p.v_str[2];
+    if (is_dk) {
+      bf16* dkp = (bf16*)p.dk + b * p.k_str[0] + h * p.k_str[1] + (int64_t)key * p.k_str[2];
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+      for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int d0 = db * 32 + 8 * c + 4 * g;
-        if (d0 < p.D) {
-          store4(dkp + d0, dk[db], 4 * c, p.scale);
-          store4(dvp + d0, dv[db], 4 * c, 1.0f);
+        for (int c = 0; c < 4; ++c) {
+          const int d0 = db * 32 + 8 * c + 4 * g;
+          if (d0 < p.D) store4(dkp + d0, acc[db], 4 * c, p.scale);
         }
-      }
+    } else {
+      bf16* dvp = (bf16*)p.dv + b * p.v_str[0] + h * p.v_str[1] + (int64_t)key * p.v_str[2];
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int d0 = db * 32 + 8 * c + 4 * g;
+          if (d0 < p.D) store4(dvp + d0, acc[db], 4 * c, 1.0f);
+        }
+    }
   }
   if constexpr (DBM == kDbColsum) {
     const float tot = colsum + shfl_xor32(colsum);
-    if (kok && g == 0) store_db(p, dbbase, tot);
+    if (is_dk && kok && g == 0) store_db(p, dbbase, tot);
   }
 }
 
@@ -498,7 +517,7 @@ template <int DP, bool HB, bool CA, int DBM>
 static void launch_dkdv_bf16_t(Params p, hipStream_t stream) {
   p.nkt = (p.Lk + 127) / 128;
   const int n = p.B * p.H * p.nkt;
-  hipLaunchKernelGGL((dkdv_bf16_kernel<DP, HB, CA, DBM>), dim3(n), dim3(256), 0,
+  hipLaunchKernelGGL((dkdv_bf16_kernel<DP, HB, CA, DBM>), dim3(n), dim3(512), 0,
                      stream, p);
 }
 

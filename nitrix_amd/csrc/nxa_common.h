@@ -239,6 +239,56 @@ __device__ __forceinline__ bf16x8 lds_tr_frag_swz(const bf16* tile, int r0,
 }
 
 // ---------------------------------------------------------------------------
+// Row-permuted, padded bf16 tiles ("P-tiles").  Logical row r lives at
+// physical row tperm(r) (a 4x4 transpose inside every group of 16 rows), rows
+// are DP + 8 elements apart (16-byte pad).  With this layout
+//   * 16-byte row reads of 16 consecutive rows hit 16 distinct 16-byte bank
+//     groups (the pad alone spreads them);
+//   * ds_read_b64_tr_b16 reads, whose 32 lanes cover 4 consecutive rows x 64
+//     bytes, see those 4 rows 64 bytes apart (the permutation);
+// and both kinds of address are one per-lane base plus compile-time
+// immediates.  Tiles are filled by 1 KB direct copies: a 64-row tile is
+// exactly 64 * (DP / 8 + 1) 16-byte slots, the pad slots receive filler.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int tperm(int r) {
+  return (r & ~15) | ((r & 3) << 2) | ((r >> 2) & 3);
+}
+
+template <int DP>
+struct PTile {
+  static constexpr int STRIDE = DP + 8;     // elements per physical row
+  static constexpr int SPR = DP / 8 + 1;    // 16-byte slots per row
+  static constexpr int ROWS = 64;
+  static constexpr int NI = ROWS * SPR / 64;  // 1 KB copies per tile
+  static constexpr int ELEMS = ROWS * STRIDE;
+  static_assert(ROWS * SPR % 64 == 0, "tile must be whole 1 KB copies");
+
+  // Element offset of the 16-byte row read (logical row, head-dim element d).
+  static __device__ __forceinline__ int row_off(int row, int d) {
+    return tperm(row) * STRIDE + d;
+  }
+};
+
+// Transposed MFMA operand fragment f from a P-tile (see lds_tr_frag for the
+// lane mapping): rows r0 + key(f, g, j), columns col0 + lane % 32.
+template <int DP>
+__device__ __forceinline__ bf16x8 ptile_tr_frag(const bf16* tile, int r0,
+                                                int col0, int lane, int f) {
+  constexpr int S = PTile<DP>::STRIDE;
+  const int grp = lane >> 4, i = lane & 15;
+  const int row = r0 + 16 * f + 4 * (grp >> 1) + (i >> 2);
+  const int col = col0 + 16 * (grp & 1) + 4 * (i & 3);
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const bf16* p0 = tile + tperm(row) * S + col;
+  const bf16* p1 = tile + tperm(row + 8) * S + col;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p1);
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  const i16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// ---------------------------------------------------------------------------
 // Direct global -> LDS copies (no staging registers).  For one wave, lane l's
 // `size` bytes land at lds + l * size; the LDS address must be wave-uniform.
 // Completion is tracked by vmcnt like any vector load.
@@ -268,6 +318,37 @@ __device__ __forceinline__ void barrier_nofence() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
+
+// Fills a 64-row P-tile from rows r0.. of a [nrows, D] bf16 matrix (row stride
+// rs elements) with 1 KB direct copies; copy j is issued by wave j % NW.
+// Rows past nrows are clamped to the last row and head-dim chunks past D (and
+// pad slots) read chunk 0 of the row: finite filler that callers mask or
+// multiply by zero.
+template <int DP, int NW>
+struct PTileCopy {
+  static constexpr int NI = PTile<DP>::NI;
+  static constexpr int CNT_HI = (NI + NW - 1) / NW;  // copies of waves < N_HI
+  static constexpr int CNT_LO = NI / NW;             // copies of the others
+  static constexpr int N_HI = NI % NW;
+
+  static __device__ __forceinline__ void issue(const bf16* src, int64_t rs,
+                                               int r0, int nrows, int D,
+                                               bf16* tile, int wave, int lane) {
+    constexpr int SPR = PTile<DP>::SPR;
+#pragma unroll
+    for (int j0 = 0; j0 < NI; j0 += NW) {
+      const int j = j0 + wave;
+      if (j < NI) {  // wave-uniform
+        const int s = j * 64 + lane;
+        const int prow = s / SPR;
+        const int k = s - prow * SPR;
+        const int row = min(r0 + tperm(prow), nrows - 1);
+        const int col = (k < SPR - 1 && k * 8 < D) ? k * 8 : 0;
+        dma16(src + (int64_t)row * rs + col, tile + j * 512);
+      }
+    }
+  }
+};
 
 __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
 __device__ __forceinline__ float to_f32(float x) { return x; }
