@@ -62,14 +62,18 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
   constexpr int EPC = 8, KC = 16;
   constexpr int BNK = 128, BQ = 64, NW = 8;
   using PT = PTile<DP>;
-  using PC = PTileCopy<DP, NW>;
+  // Only the dV waves (0-3) copy query tiles: their MFMA chain is shorter,
+  // so the copy issue (limited by the CU's address unit) fills their slack
+  // while the dK waves keep computing.
+  constexpr int NCW = 4;
+  using PC = PTileCopy<DP, NCW>;
   constexpr int NC = DP / KC, NDB = DP / 32;
   constexpr int FPB = M::FRAGS_PER_BLOCK;
   // copies per wave per query tile (Q, dO, lse2, delta)
   constexpr int LPT_HI = 2 * PC::CNT_HI + 2, LPT_LO = 2 * PC::CNT_LO + 2;
   static_assert(PT::ROWS == BQ, "tile / block mismatch");
   __shared__ __attribute__((aligned(16))) bf16 tiles[3][2][PT::ELEMS];
-  __shared__ __attribute__((aligned(16))) float rowv[3][NW][2][BQ];
+  __shared__ __attribute__((aligned(16))) float rowv[3][NCW][2][BQ];
   __shared__ uint8_t tcls[kMaxBwdTiles];
 
   const int nblk = p.B * p.H * p.nkt;
@@ -153,9 +157,9 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
   // to cover them (vmcnt there only tracks the tile copies).
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
-  // Copies of query tile t into ring stage st.  Rows past Lq are clamped to
-  // the last row and head-dim chunks past D to chunk 0 (finite values that
-  // the keep-mask or the zero K / V columns cancel).
+  // Copies of query tile t into ring stage st (dV waves only).  Rows past Lq
+  // are clamped to the last row and head-dim chunks past D to chunk 0 (finite
+  // values that the keep-mask or the zero K / V columns cancel).
   auto issue = [&](int t, int st) {
     const int q0 = t * BQ;
     PC::issue(qp, qs, q0, p.Lq, p.D, &tiles[st][0][0], wave, lane);
@@ -181,21 +185,24 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
     constexpr bool DK = decltype(role_tag)::value;
     int cur = next_active(0);
     int nxt = cur < nq ? next_active(cur + 1) : nq;
-    if (cur < nq) issue(cur, 0);
-    if (nxt < nq) issue(nxt, 1);
-    wait_tiles(nxt < nq);
+    if constexpr (!DK) {
+      if (cur < nq) issue(cur, 0);
+      if (nxt < nq) issue(nxt, 1);
+      wait_tiles(nxt < nq);
+    }
     barrier_nofence();
     int st = 0;
 
     while (cur < nq) {
       const int nxt2 = nxt < nq ? next_active(nxt + 1) : nq;
-      if (nxt2 < nq) issue(nxt2, st == 0 ? 2 : st - 1);
+      if constexpr (!DK)
+        if (nxt2 < nq) issue(nxt2, st == 0 ? 2 : st - 1);
 
       const int cls = tclass(cur);
       const bf16* Qs = tiles[st][0];
       const bf16* Ds = tiles[st][1];
-      const float* lse2s = rowv[st][wave][0];
-      const float* dlts = rowv[st][wave][1];
+      const float* lse2s = rowv[st][wave & 3][0];
+      const float* dlts = rowv[st][wave & 3][1];
       const int q0 = cur * BQ;
       const bool need_mask = p.has_mask && !(cls & 2);
       const bool tail = (q0 + BQ > p.Lq) || (kw0 + 32 > p.Lk);
@@ -280,7 +287,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
       }
 
       // Tile nxt must be resident before the barrier; nxt2 may stay in flight.
-      wait_tiles(nxt2 < nq);
+      if constexpr (!DK) wait_tiles(nxt2 < nq);
       barrier_nofence();
       st = st == 2 ? 0 : st + 1;
       cur = nxt;
