@@ -22,6 +22,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Lambdas used several times in a kernel body must still be inlined: an
+// outlined call would spill the accumulators through the call ABI.
+#define NXA_INLINE __attribute__((always_inline))
+
 namespace nxa {
 
 typedef __bf16 bf16;
@@ -293,13 +297,25 @@ __device__ __forceinline__ bf16x8 ptile_tr_frag(const bf16* tile, int r0,
 // `size` bytes land at lds + l * size; the LDS address must be wave-uniform.
 // Completion is tracked by vmcnt like any vector load.
 // ---------------------------------------------------------------------------
+//
+// The copies are written as inline assembly on purpose: the compiler treats
+// its own LDS-DMA builtin as a store to all of LDS and waits for vmcnt(0)
+// before the next LDS read, which would drain every prefetch in flight.
+// Callers order the copies themselves: a vmcnt wait for their own copies,
+// then a barrier, before anyone reads the destination.  M0 carries the LDS
+// base; one wait state separates its write from the copy.
+__device__ __forceinline__ uint32_t lds_offset(const void* lds) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
+}
 __device__ __forceinline__ void dma16(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(
-      g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_offset(lds));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(g), "s"(m) : "m0");
 }
 __device__ __forceinline__ void dma4(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(
-      g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_offset(lds));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(g), "s"(m) : "m0");
 }
 
 // s_waitcnt immediate that waits for vmcnt <= n and leaves expcnt / lgkmcnt

@@ -61,7 +61,8 @@ __global__ __launch_bounds__(256) void tilemap_kernel(const Params p, int MB,
 }
 
 // ---------------------------------------------------------------------------
-// Forward kernel.  Block = 4 waves x 32 queries (128 rows); two blocks share
+// Forward kernel (fp32 I/O; bf16 I/O has its own kernel with direct
+// global->LDS tile copies).  Block = 4 waves x 32 queries (128 rows); two blocks share
 // a CU, so one block's softmax (VALU, v_exp) overlaps the other's MFMAs.
 // 64-key K/V tiles stream through double-buffered LDS: the next tile is
 // fetched into registers while the current one is consumed.
@@ -355,8 +356,7 @@ static void launch_fwd_flags(const Params& p, hipStream_t stream) {
 
 void launch_fwd(const Params& p, int io_dtype, int dp, hipStream_t stream) {
   if (io_dtype == kBF16) {
-    if (dp == 64) launch_fwd_flags<bf16, 64>(p, stream);
-    else launch_fwd_flags<bf16, 128>(p, stream);
+    launch_fwd_bf16(p, dp, stream);
   } else {
     if (dp == 64) launch_fwd_flags<float, 64>(p, stream);
     else launch_fwd_flags<float, 128>(p, stream);
