@@ -335,6 +335,66 @@ __device__ __forceinline__ void barrier_nofence() {
   asm volatile("" ::: "memory");
 }
 
+// Direct copy of 16 bytes per lane to LDS byte offset `lds` (wave-uniform).
+__device__ __forceinline__ void dma16_at(const void* g, uint32_t lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(g), "s"(m) : "m0");
+}
+
+// Streams 64-row P-tiles of one [nrows, D] bf16 matrix (row stride rs
+// elements) into LDS.  Copy j of a tile is issued by wave (j + rot) % NW; the
+// lane's source offset inside the tile (row * rs + column) is computed once,
+// so a tile costs one 64-bit add per copy.  Rows past nrows are clamped to
+// the last row (only in the tail tile) and head-dim chunks past D (and pad
+// slots) read chunk 0 of the row: finite filler that callers mask or multiply
+// by zero.
+template <int DP, int NW>
+struct PTileStream {
+  static constexpr int NI = PTile<DP>::NI;
+  static constexpr int CNT = (NI + NW - 1) / NW;  // copies per wave (at most)
+  int64_t off[CNT];
+  int row[CNT];
+  int col[CNT];
+  int me;  // this wave's slot in the copy rotation
+
+  __device__ __forceinline__ void init(int64_t rs, int D, int wave, int rot,
+                                       int lane) {
+    constexpr int SPR = PTile<DP>::SPR;
+    me = (wave + NW - rot) % NW;
+#pragma unroll
+    for (int m = 0; m < CNT; ++m) {
+      const int s = (m * NW + me) * 64 + lane;
+      const int prow = s / SPR;
+      const int k = s - prow * SPR;
+      row[m] = tperm(prow);
+      col[m] = (k < SPR - 1 && k * 8 < D) ? k * 8 : 0;
+      off[m] = (int64_t)row[m] * rs + col[m];
+    }
+  }
+  // Number of copies this wave issues per tile.
+  __device__ __forceinline__ int count() const { return me < NI % NW ? CNT : NI / NW; }
+
+  // Copies rows r0.. of `src` into the tile at LDS byte offset `lds`.
+  __device__ __forceinline__ void issue(const bf16* src, int64_t rs, int r0,
+                                        int nrows, uint32_t lds) const {
+    if (r0 + 64 <= nrows) {
+      const bf16* base = src + (int64_t)r0 * rs;
+#pragma unroll
+      for (int m = 0; m < CNT; ++m)
+        if (m * NW + me < NI)  // wave-uniform
+          dma16_at(base + off[m], lds + (m * NW + me) * 1024);
+    } else {
+#pragma unroll
+      for (int m = 0; m < CNT; ++m)
+        if (m * NW + me < NI) {
+          const int r = min(r0 + row[m], nrows - 1);
+          dma16_at(src + (int64_t)r * rs + col[m], lds + (m * NW + me) * 1024);
+        }
+    }
+  }
+};
+
 // Fills a 64-row P-tile from rows r0.. of a [nrows, D] bf16 matrix (row stride
 // rs elements) with 1 KB direct copies; copy j is issued by wave j % NW.
 // Rows past nrows are clamped to the last row and head-dim chunks past D (and

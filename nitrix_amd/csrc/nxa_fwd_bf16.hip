@@ -46,13 +46,9 @@ __global__ __launch_bounds__(512, 1) void fwd_bf16_kernel(const Params p) {
   constexpr int EPC = 8, KC = 16;
   constexpr int NW = 8, BM = NW * 32, BN = 64, NST = 4;
   using PT = PTile<DP>;
-  using PC = PTileCopy<DP, NW>;
+  using PS = PTileStream<DP, NW>;
   constexpr int NC = DP / KC, NDB = DP / 32, FPB = M::FRAGS_PER_BLOCK;
   static_assert(PT::ROWS == BN, "tile / block mismatch");
-  // Copies per wave per tile: K copy j is issued by wave j % 8, V copy j by
-  // wave 7 - j % 8, so the odd copy of each lands on wave 0 and wave 7.
-  constexpr int CPT_EDGE = PC::CNT_HI + PC::CNT_LO;
-  constexpr int CPT_MID = 2 * PC::CNT_LO;
   __shared__ __attribute__((aligned(16))) bf16 tiles[NST][2][PT::ELEMS];
   __shared__ uint16_t act[kFwdMaxTiles];  // active key tiles, in order
   __shared__ uint8_t acls[kFwdMaxTiles];  // their classes
@@ -63,7 +59,8 @@ __global__ __launch_bounds__(512, 1) void fwd_bf16_kernel(const Params p) {
   const int bh = vid / p.nqt;
   const int qt = p.nqt - 1 - (vid % p.nqt);  // longest (causal) tiles first
   const int b = bh / p.H, h = bh % p.H;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
   const int g = lane >> 5, c32 = lane & 31;
   const int q0 = qt * BM;
   const int qw0 = q0 + wave * 32;
@@ -99,7 +96,9 @@ __global__ __launch_bounds__(512, 1) void fwd_bf16_kernel(const Params p) {
   }
   __syncthreads();
   const int n = listed ? nact_s : nkt;
-  auto tile_of = [&](int i) NXA_INLINE -> int { return listed ? (int)act[i] : i; };
+  // Contiguous active tiles (no mask, key padding, causal) need no lookup.
+  const bool dense = !listed || n == 0 || act[n - 1] == n - 1;
+  auto tile_of = [&](int i) NXA_INLINE -> int { return dense ? i : (int)act[i]; };
   auto class_of = [&](int i) NXA_INLINE -> int { return listed ? (int)acls[i] : class_g(i); };
 
   // --- stationary Q^T fragments ----------------------------------------------
@@ -135,20 +134,31 @@ __global__ __launch_bounds__(512, 1) void fwd_bf16_kernel(const Params p) {
   // Copies of the i-th active tile into ring stage st.  Keys past Lk are
   // clamped to the last key (masked below) and head-dim chunks past D read
   // chunk 0 (multiplied by Q's zero columns, or landing in unstored O rows).
+  // K copy j is issued by wave j % 8 and V copy j by wave (j + 4) % 8, so the
+  // odd copy of each (17 per tile at D = 128) lands on different waves.
+  PS ksm, vsm;
+  ksm.init(ks, p.D, wave, 0, lane);
+  vsm.init(vs, p.D, wave, NW / 2, lane);
+  const int my_copies = ksm.count() + vsm.count();  // wave-uniform
+  const uint32_t lds0 = lds_offset(&tiles[0][0][0]);
+  constexpr uint32_t kTileBytes = PT::ELEMS * 2;
   auto issue = [&](int i, int st) NXA_INLINE {
     const int k0 = tile_of(i) * BN;
-    PC::issue(kp, ks, k0, p.Lk, p.D, &tiles[st][0][0], wave, lane);
-    PC::issue(vp, vs, k0, p.Lk, p.D, &tiles[st][1][0], NW - 1 - wave, lane);
+    const uint32_t at = lds0 + st * 2 * kTileBytes;
+    ksm.issue(kp, ks, k0, p.Lk, at);
+    vsm.issue(vp, vs, k0, p.Lk, at + kTileBytes);
   };
   // Waits for this wave's copies of the oldest tile in flight (more = a
   // later tile is in flight too).
   auto wait_tile = [&](bool more) NXA_INLINE {
     if (!more)
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    else if (wave == 0 || wave == NW - 1)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(CPT_EDGE));
+    else if (my_copies == 2 * PS::CNT)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PS::CNT));
+    else if (my_copies == 2 * PS::CNT - 1)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PS::CNT - 1));
     else
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(CPT_MID));
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PS::CNT - 2));
   };
   // A tile holds nothing for this wave when all its keys are past the
   // wave's last query (causal) or the wave has no query rows.
