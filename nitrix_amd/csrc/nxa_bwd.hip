@@ -127,8 +127,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) T Dt[DP * ST];
   __shared__ float lse_s[BQ], dlt_s[BQ];
 
-  const int nblk = p.B * p.H * p.nkt;
-  const int vid = xcd_remap(blockIdx.x, nblk);
+  const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nkt);
   const int bh = vid / p.nkt;
   const int kt = vid % p.nkt;
   const int b = bh / p.H, h = bh % p.H;
@@ -302,8 +301,7 @@ __global__ __launch_bounds__(256) void dq_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) T Vs[BN * SK];
   __shared__ __attribute__((aligned(16))) T Kt[DP * ST];
 
-  const int nblk = p.B * p.H * p.nqt;
-  const int vid = xcd_remap(blockIdx.x, nblk);
+  const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
   const int bh = vid / p.nqt;
   const int qt = p.nqt - 1 - (vid % p.nqt);
   const int b = bh / p.H, h = bh % p.H;

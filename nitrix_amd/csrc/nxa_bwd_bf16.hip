@@ -76,8 +76,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) float rowv[3][NCW][2][BQ];
   __shared__ uint8_t tcls[kMaxBwdTiles];
 
-  const int nblk = p.B * p.H * p.nkt;
-  const int vid = xcd_remap(blockIdx.x, nblk);
+  const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nkt);
   const int bh = vid / p.nkt;
   const int kt = vid % p.nkt;
   const int b = bh / p.H, h = bh % p.H;
@@ -349,8 +348,7 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) bf16 tiles[2][2][TSZ];  // [stage][K|V]
   __shared__ uint8_t tcls[kMaxBwdTiles];
 
-  const int nblk = p.B * p.H * p.nqt;
-  const int vid = xcd_remap(blockIdx.x, nblk);
+  const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
   const int bh = vid / p.nqt;
   const int qt = p.nqt - 1 - (vid % p.nqt);
   const int b = bh / p.H, h = bh % p.H;

@@ -522,13 +522,17 @@ __device__ __forceinline__ int tile_class(const Params& p, int b, int h,
   return any | (all << 1);
 }
 
-// Maps a linear block id so that consecutive virtual ids land on the same
-// XCD (blocks are dispatched round-robin over the 8 XCDs): blocks that share
-// K/V (same batch and head) then share one L2.
-__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+// Maps a linear block id to a virtual id head * ntiles + tile.  Blocks are
+// dispatched round-robin over the 8 XCDs, so block b runs on XCD b % 8; this
+// map gives XCD x the heads x, x + 8, x + 16, ... whole: the blocks of one
+// (batch, head), which share K / V, share one L2, and every XCD gets the same
+// mix of batches (sequence lengths differ between batches, so handing an XCD
+// a contiguous range of heads -- a whole batch -- would unbalance them).
+__device__ __forceinline__ int xcd_remap(int bid, int nheads, int ntiles) {
   constexpr int kXcd = 8;
-  if (nblocks % kXcd != 0) return bid;
-  return (bid % kXcd) * (nblocks / kXcd) + bid / kXcd;
+  if (nheads % kXcd != 0) return bid;
+  const int x = bid % kXcd, k = bid / kXcd;
+  return (x + kXcd * (k / ntiles)) * ntiles + k % ntiles;
 }
 
 }  // namespace nxa

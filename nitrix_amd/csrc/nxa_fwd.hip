@@ -100,8 +100,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) T smem[2 * (KSZ + VSZ)];
   __shared__ uint8_t tcls[kMaxTileClasses];
 
-  const int nblk = p.B * p.H * p.nqt;
-  const int vid = xcd_remap(blockIdx.x, nblk);
+  const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
   const int bh = vid / p.nqt;
   const int qt = p.nqt - 1 - (vid % p.nqt);  // longest (causal) tiles first
   const int b = bh / p.H, h = bh % p.H;

@@ -31,6 +31,8 @@ namespace nxa {
 
 constexpr int kFwdMaxTiles = 1024;       // key tiles listed in LDS per block
 constexpr float kFwdRescaleSlack = 8.0f;  // lazy max raise threshold (log2)
+// Instruction classes of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
 
 // max / sum over the two 32-lane halves (lanes l and l ^ 32).
 __device__ __forceinline__ float half_max(float x) {
@@ -54,8 +56,7 @@ __global__ __launch_bounds__(512, 1) void fwd_bf16_kernel(const Params p) {
   __shared__ uint8_t acls[kFwdMaxTiles];  // their classes
   __shared__ int nact_s;
 
-  const int nblk = p.B * p.H * p.nqt;
-  const int vid = xcd_remap(blockIdx.x, nblk);
+  const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
   const int bh = vid / p.nqt;
   const int qt = p.nqt - 1 - (vid % p.nqt);  // longest (causal) tiles first
   const int b = bh / p.H, h = bh % p.H;
@@ -168,17 +169,34 @@ __global__ __launch_bounds__(512, 1) void fwd_bf16_kernel(const Params p) {
   };
 
   // S^T = K Q^T for the tile in stage st: 64 keys (two 32-key blocks).
+  // The K fragments are read PD products ahead of their use (a rotating
+  // register buffer) to cover the LDS latency.
+  constexpr int PD = 4;
   auto qk = [&](int st) NXA_INLINE {
     const bf16* Ks = tiles[st][0];
+    auto kfrag = [&](int j) NXA_INLINE {
+      return ld16(&Ks[PT::row_off((j & 1) * 32 + c32, (j >> 1) * KC + g * EPC)]);
+    };
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+    Frag kbuf[PD];
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
+    for (int j = 0; j < PD; ++j) kbuf[j] = kfrag(j);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-        M::run(s[kb], ld16(&Ks[PT::row_off(kb * 32 + c32, c * KC + g * EPC)]), qf[c]);
+    for (int j = 0; j < 2 * NC; ++j) {
+      M::run(s[j & 1], kbuf[j % PD], qf[j >> 1]);
+      if (j + PD < 2 * NC) kbuf[j % PD] = kfrag(j + PD);
+    }
+    // Keep that order: PD reads, then one product and one read at a time.
+#pragma unroll
+    for (int j = 0; j < PD; ++j) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+#pragma unroll
+    for (int j = 0; j < 2 * NC; ++j) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      if (j + PD < 2 * NC) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
   };
 
   // Softmax of the i-th active tile (scores in s) and O^T += V^T P^T.
@@ -247,15 +265,30 @@ __global__ __launch_bounds__(512, 1) void fwd_bf16_kernel(const Params p) {
     l_i += rs;
 
     const bf16* Vs = tiles[st][1];
+    // Product j: key block kb = j / (FPB NDB), fragment f, head-dim block db.
+    constexpr int NPV = 2 * FPB * NDB;
+    auto vfrag = [&](int j) NXA_INLINE {
+      return ptile_tr_frag<DP>(Vs, (j / (FPB * NDB)) * 32, (j % NDB) * 32, lane,
+                               (j / NDB) % FPB);
+    };
+    Frag vbuf[PD];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int j = 0; j < PD; ++j) vbuf[j] = vfrag(j);
+    Frag pf;
 #pragma unroll
-      for (int f = 0; f < FPB; ++f) {
-        const Frag pf = M::pack(s[kb], f);
+    for (int j = 0; j < NPV; ++j) {
+      if (j % NDB == 0) pf = M::pack(s[j / (FPB * NDB)], (j / NDB) % FPB);
+      M::run(oacc[j % NDB], vbuf[j % PD], pf);
+      if (j + PD < NPV) vbuf[j % PD] = vfrag(j + PD);
+    }
+    // Each V fragment is two transposed reads.
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
-          M::run(oacc[db], ptile_tr_frag<DP>(Vs, kb * 32, db * 32, lane, f), pf);
-      }
+    for (int j = 0; j < PD; ++j) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+#pragma unroll
+    for (int j = 0; j < NPV; ++j) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      if (j + PD < NPV) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+    }
   };
 
   auto run = [&](auto lag_tag) {
