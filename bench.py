@@ -1,31 +1,45 @@
 """Benchmark of the fused attention hot path on one MI355X.
 
-Workload (the configuration the headline metric is quoted on): bf16
-fwd+bwd, B=8, H=16, L=4096, D=128, q/k/v/dO ~ N(0,1), key-padding keep-mask
-[8,1,1,4096] whose per-batch valid length is drawn uniformly from
-[1024, 4096], no bias, scale 1/sqrt(D).  One step = one forward + one
-backward through the public drop-in (autograd over the C ABI), inputs
-resident in HBM.
+Default workload (``--config c2``, the configuration the headline metric is
+quoted on, BASELINE ``configs[1]``): bf16 fwd+bwd, B=8, H=16, L=4096, D=128,
+q/k/v/dO ~ N(0,1), key-padding keep-mask [8,1,1,4096] whose per-batch valid
+length is drawn uniformly from [1024, 4096], no bias, scale 1/sqrt(D).  One
+step = one forward + one backward through the public drop-in (autograd over
+the C ABI), inputs resident in HBM.
+
+The other BASELINE configurations are available as ``--config c1|c3|c4|c5``
+(one JSON line per run, same keys):
+
+* ``c1`` fp32 fwd, B1 H4 L256 D64, full bias [1,4,256,256];
+* ``c3`` bf16 causal fwd+bwd, B4 H32 L8192 D128;
+* ``c4`` bf16 fwd, full per-head bias [2,16,8192,8192], q/k/v [2,16,8192,64]
+  (HBM-bound: ``roofline`` is GB/s against 8 TB/s);
+* ``c5`` bf16 fwd+bwd, B1 H8 L32768 D64, block-sparse keep-mask [1,1,L,L]
+  from 128x128 blocks kept with p=0.25 (diagonal kept), bias [1,8,1,L]
+  (with its gradient).
 
 Counted FLOPs follow the flash-attention convention over *kept* (query, key)
-pairs only: 4*D per pair forward (QK^T, PV) and 10*D backward, so 14*D per
-pair per step.  ``value`` is counted TFLOP/s of the whole step.
+pairs only: 4*D per pair forward (QK^T, PV) and 10*D backward.  ``value`` is
+counted TFLOP/s of the whole step.
 
 ``roofline`` is for the dominant kernel (the largest total time in the
-timed step), timed live with HIP events recorded on the launch stream by the
-library's profiling hook; its algorithmic FLOPs per launch are the GEMM work
-that kernel does on kept pairs (dK/dV kernel: S, dP, dV, dK = 8*D per pair;
-dQ kernel: S, dP, dQ = 6*D; forward: 4*D).
+step), timed live with HIP events recorded on the launch stream by the
+library's profiling hook.  MFMA-bound kernels count the GEMM work they do on
+kept pairs (dK/dV: S, dP, dV, dK = 8*D per pair; dQ: S, dP, dQ = 6*D;
+forward: 4*D); the HBM-bound biased forward counts its compulsory bytes
+(bias, q, k, v, o, lse once).
 
 ``cpu_baseline`` times the CPU oracle (numpy restatement of the reference's
-attention, forward + closed-form backward, float32) on a bounded sample of
-(batch, head) slices of the same workload on this host.
+attention, forward [+ closed-form backward], float32) on a bounded sample of
+the same workload -- blocks of query rows of single (batch, head) slices --
+and reports it in the same counted-FLOP unit.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -37,61 +51,224 @@ if _ROOT not in sys.path:
     sys.path.insert(0, _ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_F32_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0
-
-B, H, L, D = 8, 16, 4096, 128
 SEED = 2024
 
+METRIC = 'attention fwd+bwd TFLOP/s and % of bf16 MFMA peak at B8 H16 L4096 D128'
 
-def _valid_lengths():
+CONFIGS = {
+    'c1': dict(
+        io='f32', B=1, H=4, L=256, D=64, bias='full', mask=None, causal=False,
+        bwd=False,
+        workload='fp32 attention fwd, full bias [1,4,256,256] (BASELINE configs[0])',
+    ),
+    'c2': dict(
+        io='bf16', B=8, H=16, L=4096, D=128, bias=None, mask='keypad', causal=False,
+        bwd=True,
+        workload='bf16 attention fwd+bwd, key-padding mask (BASELINE configs[1])',
+    ),
+    'c3': dict(
+        io='bf16', B=4, H=32, L=8192, D=128, bias=None, mask=None, causal=True,
+        bwd=True,
+        workload='bf16 causal attention fwd+bwd (BASELINE configs[2])',
+    ),
+    'c4': dict(
+        io='bf16', B=2, H=16, L=8192, D=64, bias='full', mask=None, causal=False,
+        bwd=False,
+        workload='bf16 attention fwd, full per-head bias [2,16,8192,8192] (BASELINE configs[3])',
+    ),
+    'c5': dict(
+        io='bf16', B=1, H=8, L=32768, D=64, bias='row', mask='blocksparse', causal=False,
+        bwd=True,
+        workload='bf16 attention fwd+bwd, block-sparse mask [1,1,L,L] (128x128 blocks, '
+        'p=0.25, diagonal kept), bias [1,8,1,L] (BASELINE configs[4])',
+    ),
+}
+
+
+def _valid_lengths(B, L):
     rng = np.random.Generator(np.random.PCG64(SEED))
     return rng.integers(1024, L + 1, size=B)
 
 
-def _cpu_baseline(valid, budget_s: float = 12.0):
-    """Oracle fwd+bwd on (b, h) slices until ~budget_s of CPU time."""
-    from oracle import attention as O
+def _sparse_blocks(L):
+    """Keep-map of 128x128 blocks: kept with p=0.25, diagonal always kept."""
+    nb = L // 128
+    rng = np.random.Generator(np.random.PCG64(SEED + 7))
+    blk = rng.random((nb, nb)) < 0.25
+    blk[np.arange(nb), np.arange(nb)] = True
+    return blk
 
+
+def _blas_threads() -> int:
     try:
         from threadpoolctl import threadpool_info
 
-        cores = max(
+        return max(
             (i.get('num_threads', 1) for i in threadpool_info()
              if i.get('user_api') == 'blas'),
             default=1,
         )
     except Exception:  # pragma: no cover
-        cores = 1
+        return 1
+
+
+def _cpu_baseline(name, cfg, budget_s: float = 12.0):
+    """Oracle fwd [+ bwd] on blocks of query rows of single (b, h) slices of
+    the workload until ~budget_s of CPU time; counted FLOPs as the GPU line."""
+    from oracle import attention as O
+
+    B, H, L, D = cfg['B'], cfg['H'], cfg['L'], cfg['D']
+    bf = cfg['io'] == 'bf16'
     rng = np.random.Generator(np.random.PCG64(SEED + 1))
-    scale = 1.0 / np.sqrt(D)
+    scale = 1.0 / math.sqrt(D)
+    rows = min(L, 1024)
+    valid = _valid_lengths(B, L) if cfg['mask'] == 'keypad' else None
+    blk = _sparse_blocks(L) if cfg['mask'] == 'blocksparse' else None
+    per_pair = 14.0 * D if cfg['bwd'] else 4.0 * D
+
+    def draw(shape):
+        x = rng.standard_normal(shape, dtype=np.float32)
+        return O.round_bf16(x) if bf else x
+
+    def sample(n):
+        b = n % B
+        r0 = (n * rows) % L
+        q = draw((1, 1, rows, D))
+        k = draw((1, 1, L, D))
+        v = draw((1, 1, L, D))
+        g = draw((1, 1, rows, D))
+        bias = None
+        mask = None
+        if cfg['bias'] == 'full':
+            bias = draw((1, 1, rows, L))
+        elif cfg['bias'] == 'row':
+            bias = draw((1, 1, 1, L))
+        if cfg['mask'] == 'keypad':
+            mask = (np.arange(L) < valid[b])[None, None, None, :]
+        elif cfg['mask'] == 'blocksparse':
+            rb = np.repeat(blk[r0 // 128:(r0 + rows) // 128], 128, axis=0)
+            mask = np.repeat(rb, 128, axis=1)[None, None]
+        if cfg['causal']:
+            cm = (np.arange(r0, r0 + rows)[:, None] >= np.arange(L)[None, :])
+            mask = cm[None, None] if mask is None else (mask & cm)
+        kept = (
+            float(np.broadcast_to(mask, (1, 1, rows, L)).sum())
+            if mask is not None else float(rows * L)
+        )
+        return q, k, v, g, bias, mask, kept
+
+    # Inputs are drawn before the clock starts; only oracle calls are timed.
+    samples = [sample(i) for i in range(min(B, 4) if L > 256 else B * H)]
     flops = 0.0
     n = 0
-    t0 = time.perf_counter()
-    while True:
-        b = n % B
-        q = O.round_bf16(rng.standard_normal((1, 1, L, D), dtype=np.float32))
-        k = O.round_bf16(rng.standard_normal((1, 1, L, D), dtype=np.float32))
-        v = O.round_bf16(rng.standard_normal((1, 1, L, D), dtype=np.float32))
-        g = O.round_bf16(rng.standard_normal((1, 1, L, D), dtype=np.float32))
-        mask = (np.arange(L) < valid[b])[None, None, None, :]
-        O.sdpa_forward(q, k, v, mask=mask, scale=scale)
-        O.sdpa_backward(q, k, v, g, mask=mask, scale=scale)
-        flops += 14.0 * D * L * float(valid[b])
+    dt = 0.0
+    while dt < budget_s:
+        q, k, v, g, bias, mask, kept = samples[n % len(samples)]
+        t0 = time.perf_counter()
+        O.sdpa_forward(q, k, v, bias=bias, mask=mask, scale=scale)
+        if cfg['bwd']:
+            O.sdpa_backward(q, k, v, g, bias=bias, mask=mask, scale=scale)
+        dt += time.perf_counter() - t0
+        flops += per_pair * kept
         n += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    dt = time.perf_counter() - t0
+    what = 'fwd+bwd' if cfg['bwd'] else 'fwd'
     return {
         'value': flops / dt / 1e12,
         'unit': 'TFLOP/s',
-        'cores': int(cores),
+        'cores': int(_blas_threads()),
         'kind': 'port',
         'sample': (
-            f'{n} (b,h) slices of the workload (L={L}, D={D}, key-padding '
-            f'mask of batch b), numpy oracle fwd+bwd in float32, {dt:.1f} s; '
-            f'counted FLOPs as the GPU line'
+            f'{n} blocks of {rows} query rows x {L} keys of single (b,h) slices of '
+            f'the {name} workload (same mask/bias/causal structure), numpy oracle '
+            f'{what} in float32, {dt:.1f} s; counted FLOPs as the GPU line'
         ),
     }
+
+
+class Workload:
+    """Device inputs of one configuration plus its counted work."""
+
+    def __init__(self, name, cfg, torch, dev):
+        self.name, self.cfg = name, cfg
+        B, H, L, D = cfg['B'], cfg['H'], cfg['L'], cfg['D']
+        dtype = torch.bfloat16 if cfg['io'] == 'bf16' else torch.float32
+        self.dtype = dtype
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(SEED)
+
+        def randn(*shape, grad=False):
+            x = torch.empty(*shape, device=dev, dtype=dtype)
+            flat = x.view(-1)
+            step = 1 << 28
+            for i in range(0, flat.numel(), step):
+                n = min(step, flat.numel() - i)
+                flat[i:i + n] = torch.randn(n, generator=gen, device=dev, dtype=torch.float32)
+            return x.requires_grad_(grad)
+
+        bwd = cfg['bwd']
+        self.q = randn(B, H, L, D, grad=bwd)
+        self.k = randn(B, H, L, D, grad=bwd)
+        self.v = randn(B, H, L, D, grad=bwd)
+        self.dout = randn(B, H, L, D) if bwd else None
+        self.bias = None
+        self.mask = None
+        desc = {}
+        if cfg['bias'] == 'full':
+            self.bias = randn(B, H, L, L)
+            desc['bias'] = f'full [{B},{H},{L},{L}] {cfg["io"]}'
+        elif cfg['bias'] == 'row':
+            self.bias = randn(1, H, 1, L, grad=bwd)
+            desc['bias'] = f'[1,{H},1,{L}] {cfg["io"]}' + (' (with dbias)' if bwd else '')
+        if cfg['mask'] == 'keypad':
+            valid = _valid_lengths(B, L)
+            self.mask = (
+                torch.arange(L, device=dev)[None, :]
+                < torch.as_tensor(valid, device=dev)[:, None]
+            )[:, None, None, :]
+            kept = float(H * L * int(valid.sum()))
+            desc['mask'] = f'key-padding [{B},1,1,{L}], valid lengths {valid.tolist()}'
+        elif cfg['mask'] == 'blocksparse':
+            blk = _sparse_blocks(L)
+            tb = torch.as_tensor(blk, device=dev)
+            self.mask = tb.repeat_interleave(128, 0).repeat_interleave(128, 1)[None, None]
+            kept = float(H * int(blk.sum()) * 128 * 128)
+            desc['mask'] = (
+                f'block-sparse [1,1,{L},{L}] bool, {int(blk.sum())} of {blk.size} '
+                f'128x128 blocks kept'
+            )
+        elif cfg['causal']:
+            kept = float(B * H * L * (L + 1) // 2)
+        else:
+            kept = float(B * H * L * L)
+        self.kept = kept
+        self.desc = desc
+        self.fwd_flops = 4.0 * D * kept
+        self.step_flops = (14.0 if bwd else 4.0) * D * kept
+        el = 2 if dtype == torch.bfloat16 else 4
+        qkvo = 4 * B * H * L * D * el
+        self.fwd_bytes = qkvo + B * H * L * 4 + (
+            self.bias.numel() * self.bias.element_size() if self.bias is not None else 0
+        ) + (self.mask.numel() if cfg['mask'] == 'blocksparse' else 0)
+
+    def step(self, sdpa):
+        c = self.cfg
+        if c['bwd']:
+            for t in (self.q, self.k, self.v, self.bias):
+                if t is not None:
+                    t.grad = None
+            out = sdpa(self.q, self.k, self.v, bias=self.bias, mask=self.mask,
+                       causal=c['causal'], backend='hip')
+            out.backward(self.dout)
+        else:
+            sdpa(self.q, self.k, self.v, bias=self.bias, mask=self.mask,
+                 causal=c['causal'], backend='hip')
+
+    def check_finite(self, torch):
+        if self.cfg['bwd']:
+            for t in (self.q, self.k, self.v):
+                assert torch.isfinite(t.grad.float()).all(), 'non-finite gradient'
 
 
 def main() -> int:
@@ -99,6 +276,7 @@ def main() -> int:
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--config', choices=sorted(CONFIGS), default='c2')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument(
         '--copy-calibration',
@@ -136,35 +314,18 @@ def main() -> int:
     _lib.lib()
     dev = torch.device('cuda:0')
     torch.cuda.set_device(dev)
-    valid = _valid_lengths()
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(SEED)
-
-    def randn(*shape):
-        return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32).to(
-            torch.bfloat16
-        )
-
-    q = randn(B, H, L, D).requires_grad_()
-    k = randn(B, H, L, D).requires_grad_()
-    v = randn(B, H, L, D).requires_grad_()
-    dout = randn(B, H, L, D)
-    mask = (
-        torch.arange(L, device=dev)[None, :]
-        < torch.as_tensor(valid, device=dev)[:, None]
-    )[:, None, None, :]
-    kept_pairs = float(H * L * int(valid.sum()))
-    step_flops = 14.0 * D * kept_pairs
+    name = args.config
+    cfg = CONFIGS[name]
+    wl = Workload(name, cfg, torch, dev)
+    B, H, L, D = cfg['B'], cfg['H'], cfg['L'], cfg['D']
 
     def step():
-        q.grad = k.grad = v.grad = None
-        out = scaled_dot_product_attention(q, k, v, mask=mask, backend='hip')
-        out.backward(dout)
+        wl.step(scaled_dot_product_attention)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    assert torch.isfinite(q.grad.float()).all(), 'non-finite gradient'
+    wl.check_finite(torch)
 
     stream = torch.cuda.current_stream(dev)
     e0 = torch.cuda.Event(enable_timing=True)
@@ -178,7 +339,7 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     ms = e0.elapsed_time(e1) / args.steps
-    value = step_flops / (ms * 1e-3) / 1e12
+    value = wl.step_flops / (ms * 1e-3) / 1e12
 
     # Per-kernel durations (HIP events around each launch, same stream).
     prof_steps = max(3, min(args.steps, 10))
@@ -189,24 +350,72 @@ def main() -> int:
     torch.cuda.synchronize()
     _lib.profile_enable(False)
     kernels = {}
-    for name in ('tilemap', 'fwd', 'delta', 'dkdv', 'dq'):
-        tot, n = _lib.profile_read(name)
+    for kname in ('tilemap', 'fwd', 'delta', 'dkdv', 'dq', 'dbias_reduce'):
+        tot, n = _lib.profile_read(kname)
         if n:
-            kernels[name] = {'avg_ms': tot / n, 'launches_per_step': n / prof_steps}
+            kernels[kname] = {'avg_ms': tot / n, 'launches_per_step': n / prof_steps}
     _lib.profile_reset()
+
+    peak = PEAK_BF16_TFLOPS if cfg['io'] == 'bf16' else PEAK_F32_TFLOPS
     per_pair = {'fwd': 4.0 * D, 'dkdv': 8.0 * D, 'dq': 6.0 * D}
     dom = max(
         (k_ for k_ in kernels if k_ in per_pair),
         key=lambda k_: kernels[k_]['avg_ms'] * kernels[k_]['launches_per_step'],
     )
-    dom_flops = per_pair[dom] * kept_pairs
-    achieved = dom_flops / (kernels[dom]['avg_ms'] * 1e-3) / 1e12
-    fwd_tflops = 4.0 * D * kept_pairs / (kernels['fwd']['avg_ms'] * 1e-3) / 1e12
+    fwd_s = kernels['fwd']['avg_ms'] * 1e-3
+    fwd_tflops = wl.fwd_flops / fwd_s / 1e12
+    if name == 'c4':
+        achieved = wl.fwd_bytes / fwd_s / 1e9
+        roofline = {
+            'kernel': 'fwd',
+            'bound': 'hbm',
+            'achieved': round(achieved, 2),
+            'peak': PEAK_HBM_GBS,
+            'unit': 'GB/s',
+            'frac': round(achieved / PEAK_HBM_GBS, 4),
+            'traffic': None,
+            'algorithmic_bytes': int(wl.fwd_bytes),
+        }
+    else:
+        dom_flops = per_pair[dom] * wl.kept
+        achieved = dom_flops / (kernels[dom]['avg_ms'] * 1e-3) / 1e12
+        roofline = {
+            'kernel': dom,
+            'bound': 'mfma',
+            'achieved': round(achieved, 3),
+            'peak': peak,
+            'unit': 'TFLOP/s',
+            'frac': round(achieved / peak, 4),
+            'traffic': None,
+        }
 
-    cpu = None if args.no_cpu_baseline else _cpu_baseline(valid)
+    cpu = None if args.no_cpu_baseline else _cpu_baseline(name, cfg)
 
+    what = 'fwd+bwd' if cfg['bwd'] else 'fwd'
+    metric = METRIC if name == 'c2' else (
+        f'attention {what} TFLOP/s and % of {cfg["io"]} MFMA peak at '
+        f'B{B} H{H} L{L} D{D}' + (' (and % of HBM bandwidth)' if name == 'c4' else '')
+    )
+    config = {
+        'workload': cfg['workload'],
+        'config_id': name,
+        'B': B,
+        'H': H,
+        'L': L,
+        'D': D,
+        'global_batch': B,
+        'seq_len': L,
+        'mask': wl.desc.get('mask'),
+        'bias': wl.desc.get('bias'),
+        'causal': cfg['causal'],
+        'counted_tflop_per_step': round(wl.step_flops / 1e12, 4),
+        'dense_equiv_tflop_per_step': round(
+            (14.0 if cfg['bwd'] else 4.0) * D * B * H * L * L / 1e12, 4
+        ),
+        'parallelism': 'single GPU',
+    }
     line = {
-        'metric': 'attention fwd+bwd TFLOP/s and % of bf16 MFMA peak at B8 H16 L4096 D128',
+        'metric': metric,
         'value': round(value, 3),
         'unit': 'TFLOP/s',
         'n_gpus': 1,
@@ -214,41 +423,22 @@ def main() -> int:
         'warmup': args.warmup,
         'ms_per_step': round(ms, 4),
         'wall_s_timed': round(wall, 4),
-        'pct_of_peak': round(100.0 * value / PEAK_BF16_TFLOPS, 3),
+        'pct_of_peak': round(100.0 * value / peak, 3),
         'higher_is_better': True,
         'scaling': 'weak',
         'vs_baseline': None,
-        'dtype': 'bf16',
+        'dtype': cfg['io'],
         'data': 'synthetic',
-        'config': {
-            'workload': 'bf16 attention fwd+bwd, key-padding mask (BASELINE configs[1])',
-            'B': B,
-            'H': H,
-            'L': L,
-            'D': D,
-            'global_batch': B,
-            'seq_len': L,
-            'mask': f'key-padding [8,1,1,4096], valid lengths {valid.tolist()}',
-            'bias': None,
-            'causal': False,
-            'counted_tflop_per_step': round(step_flops / 1e12, 4),
-            'dense_equiv_tflop_per_step': round(14.0 * D * B * H * L * L / 1e12, 4),
-            'parallelism': 'single GPU',
-        },
+        'config': config,
         'fwd_tflops': round(fwd_tflops, 3),
-        'fwd_pct_of_peak': round(100.0 * fwd_tflops / PEAK_BF16_TFLOPS, 3),
+        'fwd_pct_of_peak': round(100.0 * fwd_tflops / peak, 3),
         'kernels': {k_: {kk: round(vv, 5) for kk, vv in v_.items()} for k_, v_ in kernels.items()},
-        'roofline': {
-            'kernel': dom,
-            'bound': 'mfma',
-            'achieved': round(achieved, 3),
-            'peak': PEAK_BF16_TFLOPS,
-            'unit': 'TFLOP/s',
-            'frac': round(achieved / PEAK_BF16_TFLOPS, 4),
-            'traffic': None,
-        },
+        'roofline': roofline,
         'cpu_baseline': cpu,
     }
+    if name == 'c4':
+        line['fwd_hbm_gbs'] = roofline['achieved']
+        line['fwd_pct_of_hbm'] = round(100.0 * roofline['frac'], 3)
     print(json.dumps(line), flush=True)
     return 0
 
