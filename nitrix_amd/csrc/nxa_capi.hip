@@ -5,6 +5,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cmath>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -178,6 +179,40 @@ WsLayout ws_layout(const nxa_desc* d, int has_bias, int has_mask, int is_bwd) {
   return w;
 }
 
+// Round to the nearest bf16 (ties to even), returned as a float.
+float round_bf16(float x) {
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  float r;
+  std::memcpy(&r, &u, 4);
+  return r;
+}
+
+// Chooses how the bf16 forward adds the bias (nxa::FwdBias).  The MFMA modes
+// need a bf16 bias whose rows are 16-byte aligned whole 8-key chunks, and a
+// positive scale whose reciprocal splits into two normal bf16 terms h + l.
+int fwd_bias_mode(const nxa_desc* d, const void* bias, float* h, float* l) {
+  *h = *l = 0.f;
+  if (d->io_dtype != NXA_BF16 || d->bias_dtype != NXA_BF16) return nxa::kFbValu;
+  if (!(d->scale > 0.f) || !std::isfinite(d->scale)) return nxa::kFbValu;
+  const float inv = 1.0f / d->scale;
+  const float hi = round_bf16(inv);
+  const float lo = round_bf16(inv - hi);
+  if (!std::isfinite(hi) || !(std::fabs(hi) >= 1e-30f) || !(std::fabs(hi) <= 1e30f))
+    return nxa::kFbValu;
+  if (lo != 0.f && !(std::fabs(lo) >= 1e-30f)) return nxa::kFbValu;
+  if (d->Lk % 8 != 0 || !aligned(bias, 16) || d->bias_str[0] % 8 != 0 ||
+      d->bias_str[1] % 8 != 0)
+    return nxa::kFbValu;
+  *h = hi;
+  *l = lo;
+  if (d->bias_str[2] == 0 || d->Lq == 1) return nxa::kFbRow;
+  if (d->bias_str[2] % 8 != 0) return nxa::kFbValu;
+  return nxa::kFbTile;
+}
+
 nxa::Params base_params(const nxa_desc* d, const void* q, const void* k,
                         const void* v, const void* bias, const uint8_t* mask) {
   nxa::Params p;
@@ -211,6 +246,7 @@ nxa::Params base_params(const nxa_desc* d, const void* q, const void* k,
     for (int i = 0; i < 3; ++i) vec = vec && (d->bias_str[i] % 4 == 0);
     p.bias_vec = vec;
   }
+  p.fwd_bias = bias ? fwd_bias_mode(d, bias, &p.bias_h, &p.bias_l) : nxa::kFbNone;
   p.has_mask = mask != nullptr;
   if (mask) {
     bool vec = (d->Lk % 4 == 0) && aligned(mask, 4);

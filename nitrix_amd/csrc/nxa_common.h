@@ -87,7 +87,17 @@ struct Params {
   int tm_rows;         // mask rows covered by the tile map (Lq, or 1 if broadcast)
   int dbias_mode;
   int dbias_f32;       // 1: dbias points at fp32 partials, else bias dtype
+  int fwd_bias;        // FwdBias mode of the bf16 forward
+  float bias_h, bias_l;  // 1/scale = bias_h + bias_l, both bf16-exact
 };
+
+// How the bf16 forward adds the bias (chosen on the host).
+//  * kFbRow  / kFbTile: the bias enters the score accumulator through MFMA
+//    products bias^T x diag(1/scale) (1/scale split into two bf16 terms), so
+//    it costs no VALU work; kFbTile streams [query, key] bias tiles through
+//    the LDS ring, kFbRow (bias broadcast over queries) one key row per tile.
+//  * kFbValu: per-element loads and adds (fp32 bias, unaligned layouts).
+enum FwdBias : int { kFbNone = 0, kFbRow = 1, kFbTile = 2, kFbValu = 3 };
 
 // ---------------------------------------------------------------------------
 // MFMA policy per I/O type.
@@ -342,6 +352,20 @@ __device__ __forceinline__ void dma16_at(const void* g, uint32_t lds) {
                :: "v"(g), "s"(m) : "m0");
 }
 
+// Direct copies addressed as a wave-uniform base (SGPR pair) plus a per-lane
+// 32-bit byte offset (the global_load "saddr" form): no 64-bit per-lane
+// address arithmetic and no 64-bit per-lane address registers.
+__device__ __forceinline__ void dma16_sv(const void* base, uint32_t voff, uint32_t lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(base), "s"(m) : "m0");
+}
+__device__ __forceinline__ void dma4_sv(const void* base, uint32_t voff, uint32_t lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(base), "s"(m) : "m0");
+}
+
 // Streams 64-row P-tiles of one [nrows, D] bf16 matrix (row stride rs
 // elements) into LDS.  Copy j of a tile is issued by wave (j + rot) % NW; the
 // lane's source offset inside the tile (row * rs + column) is computed once,
@@ -394,6 +418,65 @@ struct PTileStream {
     }
   }
 };
+
+// Streams 64-row XOR-swizzled [64 x DP] bf16 tiles (swz_off layout, no
+// padding) of one [nrows, D] matrix (row stride rs elements) into LDS with
+// 1 KB direct copies: a tile is DP/8 copies, each covering 512/DP whole
+// rows of global memory, and every one of the NW waves issues exactly
+// CNT = DP/8/NW of them (so per-wave copy counts are compile-time).  The
+// lane's source offset inside the tile is computed once.  Rows past nrows
+// are clamped to the last row (only in the tail tile) and head-dim chunks
+// past D read chunk 0 of the row: finite filler that callers mask or
+// multiply by zero.
+template <int DP, int NW>
+struct SwzStream {
+  static constexpr int SPR = DP / 8;  // 16-byte slots per row
+  static constexpr int NI = SPR;      // 1 KB copies per 64-row tile
+  static constexpr int CNT = NI / NW;
+  static_assert(NI % NW == 0, "tile copies must split evenly over the waves");
+  // Byte offset of the lane's 16 bytes inside a full tile (64 rows times the
+  // row stride fit in 32 bits: the host bounds the row stride).
+  uint32_t off[CNT];
+
+  __device__ __forceinline__ static int row_of(int m, int wave, int lane) {
+    return ((m * NW + wave) * 64 + lane) / SPR;
+  }
+  __device__ __forceinline__ static int col_of(int m, int wave, int lane, int D) {
+    const int s = (m * NW + wave) * 64 + lane;
+    const int lc = (s % SPR) ^ swz<DP>(s / SPR);
+    return lc * 8 < D ? lc * 8 : 0;
+  }
+  __device__ __forceinline__ void init(int64_t rs, int D, int wave, int lane) {
+#pragma unroll
+    for (int m = 0; m < CNT; ++m)
+      off[m] = 2u * (uint32_t)(row_of(m, wave, lane) * rs + col_of(m, wave, lane, D));
+  }
+  // Copies rows r0.. of `src` into the tile at LDS byte offset `lds`.
+  __device__ __forceinline__ void issue(const bf16* src, int64_t rs, int r0,
+                                        int nrows, int D, uint32_t lds, int wave,
+                                        int lane) const {
+    const bf16* base = src + (int64_t)r0 * rs;  // wave-uniform
+    if (r0 + 64 <= nrows) {
+#pragma unroll
+      for (int m = 0; m < CNT; ++m) dma16_sv(base, off[m], lds + (m * NW + wave) * 1024);
+    } else {
+#pragma unroll
+      for (int m = 0; m < CNT; ++m) {
+        const int r = min(row_of(m, wave, lane), nrows - 1 - r0);
+        dma16_sv(base, 2u * (uint32_t)(r * rs + col_of(m, wave, lane, D)),
+                 lds + (m * NW + wave) * 1024);
+      }
+    }
+  }
+};
+
+// Direct copy of 4 bytes per lane to LDS byte offset `lds` (wave-uniform):
+// lane l's dword lands at lds + 4 l.
+__device__ __forceinline__ void dma4_at(const void* g, uint32_t lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(g), "s"(m) : "m0");
+}
 
 // Fills a 64-row P-tile from rows r0.. of a [nrows, D] bf16 matrix (row stride
 // rs elements) with 1 KB direct copies; copy j is issued by wave j % NW.

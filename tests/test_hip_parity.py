@@ -73,7 +73,7 @@ def _make_mask(rng, kind, B, H, s, t):
 
 
 def _check(dtype, B, H, s, t, d, *, bias_shape=None, bias_dtype=None,
-           mask_kind=None, causal=False, seed=0, grads=True):
+           mask_kind=None, causal=False, seed=0, grads=True, scale=None):
     rng = np.random.default_rng(seed)
     q = _draw(rng, (B, H, s, d), dtype)
     k = _draw(rng, (B, H, t, d), dtype)
@@ -82,7 +82,9 @@ def _check(dtype, B, H, s, t, d, *, bias_shape=None, bias_dtype=None,
     bias = None if bias_shape is None else _draw(rng, bias_shape, bdt)
     mask = _make_mask(rng, mask_kind, B, H, s, t)
     g = _draw(rng, (B, H, s, d), dtype)
-    scale = 1.0 / np.sqrt(d)
+    explicit_scale = scale
+    if scale is None:
+        scale = 1.0 / np.sqrt(d)
 
     tq, tk, tv = _to(q, dtype, grads), _to(k, dtype, grads), _to(v, dtype, grads)
     tb = None if bias is None else _to(bias, bdt, grads)
@@ -92,7 +94,8 @@ def _check(dtype, B, H, s, t, d, *, bias_shape=None, bias_dtype=None,
     print(f'[case] {dtype} B{B} H{H} s{s} t{t} d{d} bias={bias_shape} '
           f'mask={mask_kind} causal={causal} seed={seed}', flush=True)
     out = scaled_dot_product_attention(
-        tq, tk, tv, bias=tb, mask=tm, causal=causal, backend='hip'
+        tq, tk, tv, bias=tb, mask=tm, causal=causal, scale=explicit_scale,
+        backend='hip'
     )
     ref = O.sdpa_forward(q, k, v, bias=bias, mask=mask, scale=scale,
                          causal=causal, acc_dtype=np.float64)
@@ -152,6 +155,24 @@ def test_causal(dtype, s, t):
 ], ids=['full', 'batchbc', 'qbc', 'bhbc', 'headbc'])
 def test_bias_broadcast(dtype, bias_shape):
     _check(dtype, 2, 2, 192, 160, 64, bias_shape=bias_shape, seed=5)
+
+
+@pytest.mark.parametrize('d', [64, 128])
+@pytest.mark.parametrize('kind', ['full', 'qbc'])
+@pytest.mark.parametrize('causal,mask_kind,scale', [
+    (False, None, None),
+    (True, None, None),
+    (False, 'block', None),
+    (True, 'random', 0.37),
+], ids=['plain', 'causal', 'blockmask', 'causal_mask_scale'])
+def test_bf16_bias_through_mfma(d, kind, causal, mask_kind, scale):
+    """bf16 bias with Lk a multiple of 8: the forward adds the bias by MFMA
+    (bias^T x diag(1/scale), 1/scale split into two bf16 terms when it is not
+    a power of two), streamed through the LDS ring (full tiles) or as one key
+    row per tile (query-broadcast).  Lengths leave query and key tails."""
+    shape = (2, 2, 200, 136) if kind == 'full' else (1, 2, 1, 136)
+    _check(torch.bfloat16, 2, 2, 200, 136, d, bias_shape=shape,
+           mask_kind=mask_kind, causal=causal, seed=12 + d, scale=scale)
 
 
 def test_bias_fp32_with_bf16_io():
