@@ -1,0 +1,204 @@
+"""Parity at the BASELINE configurations' full sizes (GPU only).
+
+The CPU oracle cannot hold these problems whole (8.6-34 GB of fp32 logits per
+tensor), so each configuration is checked two ways on the same seeded inputs:
+
+* **sampled rows** -- the float64 oracle (``oracle/attention.py``) on a
+  handful of query rows of a few (batch, head) slices, with the full keys,
+  values, bias row and mask row of each: the output rows and the dQ rows are
+  exact functions of those rows alone (dQ_i = scale sum_j dS_ij k_j);
+* **size-independent identities** of the attention backward, exact in
+  arithmetic for every row that keeps at least one key:
+    - sum_j dS_ij = 0, hence sum_j dK_j = 0 and sum_j dbias_j = 0 (dbias
+      broadcast over queries);
+    - sum_j P_ij = 1, hence sum_j dV_j = sum_i dO_i;
+    - a key the mask removes gets dK_j = dV_j = 0 exactly.
+
+Budgets: ``max|a-b| / max|b| <= 2e-2`` for sampled bf16 rows (the north
+star's bf16 budget), ``|sum| / sum|.| <= 1e-2`` for the identities (sums of
+bf16-rounded gradients).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as O
+
+pytestmark = pytest.mark.gpu
+
+REL = 2e-2
+IDENT = 1e-2
+SEED = 77
+
+
+def _dev():
+    return torch.device('cuda:0')
+
+
+def _randn(gen, *shape, grad=False):
+    x = torch.empty(*shape, device=_dev(), dtype=torch.bfloat16)
+    flat = x.view(-1)
+    step = 1 << 28
+    for i in range(0, flat.numel(), step):
+        k = min(step, flat.numel() - i)
+        flat[i:i + k] = torch.randn(k, generator=gen, device=_dev(), dtype=torch.float32)
+    return x.requires_grad_(grad)
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _relerr(a, b):
+    return float(np.max(np.abs(a - b)) / (np.max(np.abs(b)) + 1e-30))
+
+
+def _check_rows(q, k, v, dout, out, dq, b, h, rows, *, scale, bias_row=None,
+                mask_row=None, causal=False):
+    """Oracle output and dQ of query ``rows`` of slice (b, h)."""
+    qn = _np(q[b, h, rows])[None, None]
+    kn = _np(k[b, h])[None, None]
+    vn = _np(v[b, h])[None, None]
+    L = kn.shape[2]
+    keep = np.ones((len(rows), L), bool)
+    if mask_row is not None:
+        keep &= mask_row
+    if causal:
+        keep &= np.asarray(rows)[:, None] >= np.arange(L)[None, :]
+    bias = None if bias_row is None else bias_row[None, None]
+    ref = O.sdpa_forward(qn, kn, vn, bias=bias, mask=keep[None, None], scale=scale,
+                         acc_dtype=np.float64)[0, 0]
+    got = _np(out[b, h, rows])
+    e = _relerr(got, ref)
+    assert e <= REL, f'out rows of ({b},{h}) relerr {e:.3e}'
+    if dq is not None:
+        gn = _np(dout[b, h, rows])[None, None]
+        rdq, _, _, _ = O.sdpa_backward(qn, kn, vn, gn, bias=bias, mask=keep[None, None],
+                                       scale=scale, acc_dtype=np.float64)
+        e = _relerr(_np(dq[b, h, rows]), rdq[0, 0])
+        assert e <= REL, f'dq rows of ({b},{h}) relerr {e:.3e}'
+
+
+def _identities(dk, dv, dout, live_rows, *, dbias=None, dead_keys=None):
+    """sum_j dK_j = 0, sum_j dV_j = sum_{live i} dO_i, sum_j dbias_j = 0."""
+    dk64 = dk.double()
+    s = dk64.sum(dim=2)
+    ratio = float((s.abs().max() / dk64.abs().sum(dim=2).max()).cpu())
+    assert ratio <= IDENT, f'sum_j dK_j / sum_j |dK_j| = {ratio:.3e}'
+    dv64 = dv.double()
+    want = (dout.double() * live_rows[..., None]).sum(dim=2)
+    err = float(((dv64.sum(dim=2) - want).abs().max() / dv64.abs().sum(dim=2).max()).cpu())
+    assert err <= IDENT, f'sum_j dV_j vs sum_i dO_i: {err:.3e}'
+    if dbias is not None:
+        db = dbias.double()
+        r = float((db.sum(dim=-1).abs().max() / db.abs().sum(dim=-1).max()).cpu())
+        assert r <= IDENT, f'sum_j dbias_j / sum_j |dbias_j| = {r:.3e}'
+    if dead_keys is not None:
+        assert torch.count_nonzero(dk[dead_keys]) == 0, 'masked key has dK != 0'
+        assert torch.count_nonzero(dv[dead_keys]) == 0, 'masked key has dV != 0'
+
+
+def _fwd_bwd(q, k, v, dout, **kw):
+    from nitrix_amd import scaled_dot_product_attention
+
+    out = scaled_dot_product_attention(q, k, v, backend='hip', **kw)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    return out
+
+
+def test_c2_key_padding_b8_h16_l4096_d128():
+    """bf16 fwd+bwd, key-padding mask, valid lengths
+    uniform in [1024, 4096]."""
+    B, H, L, D = 8, 16, 4096, 128
+    print(f'[case] C2 B{B} H{H} L{L} D{D} key padding', flush=True)
+    gen = torch.Generator(device=_dev())
+    gen.manual_seed(SEED)
+    rng = np.random.default_rng(SEED)
+    valid = rng.integers(1024, L + 1, size=B)
+    q, k, v = (_randn(gen, B, H, L, D, grad=True) for _ in range(3))
+    dout = _randn(gen, B, H, L, D)
+    mask = (torch.arange(L, device=_dev())[None, :]
+            < torch.as_tensor(valid, device=_dev())[:, None])[:, None, None, :]
+    out = _fwd_bwd(q, k, v, dout, mask=mask)
+    scale = 1.0 / math.sqrt(D)
+    for b, h in ((0, 0), (6, 11), (2, 15)):
+        rows = [0, 1, 777, L - 1]
+        mrow = np.arange(L) < valid[b]
+        _check_rows(q, k, v, dout, out, q.grad, b, h, rows, scale=scale, mask_row=mrow)
+    dead = ~mask[:, 0, 0, :]  # [B, L]
+    dead = dead[:, None, :].expand(B, H, L)
+    _identities(k.grad, v.grad, dout, torch.ones(B, H, L, device=_dev(), dtype=torch.float64),
+                dead_keys=dead)
+
+
+def test_c3_causal_b4_h32_l8192_d128():
+    """bf16 causal fwd+bwd."""
+    B, H, L, D = 4, 32, 8192, 128
+    print(f'[case] C3 B{B} H{H} L{L} D{D} causal', flush=True)
+    gen = torch.Generator(device=_dev())
+    gen.manual_seed(SEED + 1)
+    q, k, v = (_randn(gen, B, H, L, D, grad=True) for _ in range(3))
+    dout = _randn(gen, B, H, L, D)
+    out = _fwd_bwd(q, k, v, dout, causal=True)
+    scale = 1.0 / math.sqrt(D)
+    for b, h in ((0, 0), (3, 31)):
+        rows = [0, 63, 64, 4000, L - 1]
+        _check_rows(q, k, v, dout, out, q.grad, b, h, rows, scale=scale, causal=True)
+    _identities(k.grad, v.grad, dout, torch.ones(B, H, L, device=_dev(), dtype=torch.float64))
+
+
+def test_c4_full_bias_b2_h16_l8192_d64():
+    """bf16 fwd with a full per-head bias
+    [2,16,8192,8192] (streamed through the LDS ring, added by MFMA)."""
+    B, H, L, D = 2, 16, 8192, 64
+    print(f'[case] C4 B{B} H{H} L{L} D{D} full bias', flush=True)
+    gen = torch.Generator(device=_dev())
+    gen.manual_seed(SEED + 2)
+    q, k, v = (_randn(gen, B, H, L, D) for _ in range(3))
+    bias = _randn(gen, B, H, L, L)
+    from nitrix_amd import scaled_dot_product_attention
+
+    with torch.no_grad():
+        out = scaled_dot_product_attention(q, k, v, bias=bias, backend='hip')
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    scale = 1.0 / math.sqrt(D)
+    for b, h in ((0, 0), (1, 9), (0, 15)):
+        rows = [0, 255, 256, 5000, L - 1]
+        brow = _np(bias[b, h, rows])
+        _check_rows(q, k, v, None, out, None, b, h, rows, scale=scale, bias_row=brow)
+
+
+def test_c5_block_sparse_row_bias_b1_h8_l32768_d64():
+    """bf16 fwd+bwd, block-sparse mask [1,1,L,L] of
+    128x128 blocks kept with p=0.25 (diagonal kept), bias [1,8,1,L] with its
+    gradient (a column sum over queries)."""
+    B, H, L, D = 1, 8, 32768, 64
+    print(f'[case] C5 B{B} H{H} L{L} D{D} block-sparse + row bias', flush=True)
+    gen = torch.Generator(device=_dev())
+    gen.manual_seed(SEED + 3)
+    rng = np.random.default_rng(SEED + 3)
+    nb = L // 128
+    blk = rng.random((nb, nb)) < 0.25
+    blk[np.arange(nb), np.arange(nb)] = True
+    tb = torch.as_tensor(blk, device=_dev())
+    mask = tb.repeat_interleave(128, 0).repeat_interleave(128, 1)[None, None]
+    q, k, v = (_randn(gen, B, H, L, D, grad=True) for _ in range(3))
+    bias = _randn(gen, 1, H, 1, L, grad=True)
+    dout = _randn(gen, B, H, L, D)
+    out = _fwd_bwd(q, k, v, dout, bias=bias, mask=mask)
+    scale = 1.0 / math.sqrt(D)
+    for h in (0, 5):
+        rows = [0, 127, 128, 20000, L - 1]
+        mrows = np.repeat(np.repeat(blk[np.asarray(rows) // 128], 128, axis=1), 1, axis=0)
+        brow = _np(bias[0, h, 0])
+        _check_rows(q, k, v, dout, out, q.grad, 0, h, rows, scale=scale,
+                    bias_row=brow[None, :].repeat(len(rows), 0), mask_row=mrows)
+    _identities(k.grad, v.grad, dout, torch.ones(B, H, L, device=_dev(), dtype=torch.float64),
+                dbias=bias.grad[0, :, 0, :])
