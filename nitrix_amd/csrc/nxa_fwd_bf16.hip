@@ -80,31 +80,35 @@ __device__ __forceinline__ void vm_wait_le(int n) {
   }
 }
 
-// Ring geometry per (head-dim width, bias mode).  Ping-pong (LAG) schedule:
-// after barrier t the waves read V(t-1) and K(t) (and bias tile t), so the
-// K / V stage of tile t-2 and the bias stage of tile t-1 are free there.
-// With 4 K / V stages tile t+2 is issued after barrier t; with full bias
-// tiles LDS holds 3 K / V stages (tile t+1 issued, one ahead: K and V mostly
-// come from L2) and 3 bias stages (tile t+2, two ahead: the bias streams from
-// HBM).  In-step schedule (D = 128 with full bias tiles, two stages of each):
-// tile t+1 is issued after barrier t.
-template <int DP, int BMODE>
+// Ring geometry per (head-dim width, waves per block, bias mode).
+// Ping-pong (LAG, 8 waves) schedule: after barrier t the waves read V(t-1)
+// and K(t) (and bias tile t), so the K / V stage of tile t-2 and the bias
+// stage of tile t-1 are free there.  With 4 K / V stages tile t+2 is issued
+// after barrier t; with full bias tiles LDS holds 3 K / V stages (tile t+1
+// issued, one ahead: K and V mostly come from L2) and 3 bias stages (tile
+// t+2, two ahead: the bias streams from HBM).  In-step schedule (4-wave
+// blocks, and D = 128 with full bias tiles): tile t is read only between
+// barriers t and t+1, so the stage of tile t-1 receives tile t + NST - 1.
+template <int DP, int NW, int BMODE>
 struct FwdRing {
   static constexpr bool TILE_BIAS = BMODE == kFbTile;
-  static constexpr bool LAG = !(TILE_BIAS && DP == 128);
+  static constexpr bool LAG = NW == 8 && !(TILE_BIAS && DP == 128);
   static constexpr int NST = TILE_BIAS ? (LAG ? 3 : 2) : 4;  // K/V stages
   static constexpr int AHEAD = LAG ? NST - 2 : NST - 1;      // K/V tiles ahead
   static constexpr int NSTB = TILE_BIAS ? (LAG ? 3 : 2) : 1;  // bias stages
   static constexpr int AHEADB = TILE_BIAS ? NSTB - 1 : 0;     // bias tiles ahead
 };
 
-template <int DP, int BMODE, bool CAUSAL>
-__global__ __launch_bounds__(512, 2) void fwd_bf16_kernel(const Params p) {
+// NW waves of 32 queries per block: 8 (ping-pong pairs on each SIMD, one
+// block per CU) or 4 (two blocks per CU; for masks that vary over queries, so
+// that a block's key-tile list is that of its own 128 rows).
+template <int DP, int NW, int BMODE, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
   using M = Mma<bf16>;
   using Frag = bf16x8;
   constexpr int EPC = 8, KC = 16;
-  constexpr int NW = 8, BM = NW * 32, BN = 64;
-  using R = FwdRing<DP, BMODE>;
+  constexpr int BM = NW * 32, BN = 64;
+  using R = FwdRing<DP, NW, BMODE>;
   constexpr int NST = R::NST, AHEAD = R::AHEAD, NSTB = R::NSTB, AHEADB = R::AHEADB;
   constexpr bool VALU_BIAS = BMODE == kFbValu;
   constexpr bool MFMA_BIAS = BMODE == kFbRow || BMODE == kFbTile;
@@ -294,14 +298,24 @@ __global__ __launch_bounds__(512, 2) void fwd_bf16_kernel(const Params p) {
       }
     }
   };
-  // Tile i needs K/V(i) and bias(i).  Issued after K/V(i): K/V(i+1) (K / V
-  // two ahead) or bias(i+1) (K / V one ahead, bias two); in-step, nothing.
+  // Tile i needs K/V(i) and bias(i).  Issued after K/V(i): bias(i+1) (LAG
+  // with full bias tiles: K / V one ahead, bias two) or the K / V tiles
+  // i+1 .. i+AHEAD-1 that exist.
   auto wait_tile = [&](int i) NXA_INLINE {
-    constexpr int Y = !R::LAG ? 0 : (BMODE == kFbTile ? BT_COPIES : KV_COPIES);
-    if (Y > 0 && i + 1 < n)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(Y));
-    else
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    if constexpr (R::LAG && BMODE == kFbTile) {
+      if (i + 1 < n)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(BT_COPIES));
+      else
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    } else {
+      const int later = min(AHEAD - 1, n - 1 - i);
+      if (AHEAD > 2 && later >= 2)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * KV_COPIES));
+      else if (AHEAD > 1 && later >= 1)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(KV_COPIES));
+      else
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
   };
 
   // --- per-lane LDS read offsets (bytes) ----------------------------------------
@@ -640,27 +654,42 @@ __global__ __launch_bounds__(512, 2) void fwd_bf16_kernel(const Params p) {
   }
 }
 
-template <int DP, int BMODE, bool CA>
+template <int DP, int NW, int BMODE, bool CA>
 static void launch_fwd_bf16_t(Params p, hipStream_t stream) {
-  constexpr int BM = 256;
+  constexpr int BM = NW * 32;
   p.nqt = (p.Lq + BM - 1) / BM;
   const int n = p.B * p.H * p.nqt;
-  hipLaunchKernelGGL((fwd_bf16_kernel<DP, BMODE, CA>), dim3(n), dim3(512), 0, stream, p);
+  hipLaunchKernelGGL((fwd_bf16_kernel<DP, NW, BMODE, CA>), dim3(n), dim3(NW * 64), 0, stream,
+                     p);
 }
 
-template <int DP, int BMODE>
+template <int DP, int NW, int BMODE>
 static void launch_fwd_bf16_c(const Params& p, hipStream_t stream) {
-  if (p.causal) launch_fwd_bf16_t<DP, BMODE, true>(p, stream);
-  else launch_fwd_bf16_t<DP, BMODE, false>(p, stream);
+  if (p.causal) launch_fwd_bf16_t<DP, NW, BMODE, true>(p, stream);
+  else launch_fwd_bf16_t<DP, NW, BMODE, false>(p, stream);
+}
+
+// 4-wave blocks when the mask varies over queries (its tile map has rows) at
+// D <= 64, where two such blocks (4 K / V stages each) share a CU's LDS;
+// full bias tiles keep the 8-wave block, whose bias ring they need.
+template <int DP, int BMODE>
+static void launch_fwd_bf16_nw(const Params& p, hipStream_t stream) {
+  if constexpr (DP == 64 && BMODE != kFbTile) {
+    if (p.has_tilemap && p.tm_rows > 1) {
+      launch_fwd_bf16_c<DP, 4, BMODE>(p, stream);
+      return;
+    }
+  }
+  launch_fwd_bf16_c<DP, 8, BMODE>(p, stream);
 }
 
 template <int DP>
 static void launch_fwd_bf16_flags(const Params& p, hipStream_t stream) {
   switch (p.has_bias ? p.fwd_bias : kFbNone) {
-    case kFbRow: launch_fwd_bf16_c<DP, kFbRow>(p, stream); break;
-    case kFbTile: launch_fwd_bf16_c<DP, kFbTile>(p, stream); break;
-    case kFbValu: launch_fwd_bf16_c<DP, kFbValu>(p, stream); break;
-    default: launch_fwd_bf16_c<DP, kFbNone>(p, stream); break;
+    case kFbRow: launch_fwd_bf16_nw<DP, kFbRow>(p, stream); break;
+    case kFbTile: launch_fwd_bf16_nw<DP, kFbTile>(p, stream); break;
+    case kFbValu: launch_fwd_bf16_nw<DP, kFbValu>(p, stream); break;
+    default: launch_fwd_bf16_nw<DP, kFbNone>(p, stream); break;
   }
 }
 
