@@ -15,8 +15,9 @@
 namespace nxa {
 
 // ---------------------------------------------------------------------------
-// delta[b, h, q] = sum_d O[q, d] * dO[q, d]  (fp32), and lse2 = lse * log2(e)
-// so the backward kernels stream both per-row values straight from memory.
+// ndelta[b, h, q] = -sum_d O[q, d] * dO[q, d]  (fp32) and nlse2 = -lse * log2(e),
+// so the backward kernels stream both per-row values straight from memory
+// (negated: the bf16 kernels start their MFMA accumulators at them).
 // 16 lanes per row.
 // ---------------------------------------------------------------------------
 template <typename T>
@@ -45,8 +46,8 @@ __global__ __launch_bounds__(256) void delta_kernel(const Params p) {
   acc += __shfl_xor(acc, 2, 16);
   acc += __shfl_xor(acc, 1, 16);
   if (row < rows && sub == 0) {
-    p.delta[row] = acc;
-    p.lse2[row] = p.lse[row] * kLog2e;
+    p.ndelta[row] = -acc;
+    p.nlse2[row] = -p.lse[row] * kLog2e;
   }
 }
 
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
   const T* vp = (const T*)p.v + b * p.v_str[0] + h * p.v_str[1];
   const T* dop = (const T*)p.dout + b * p.o_str[0] + h * p.o_str[1];
   const float* lsep = p.lse + ((int64_t)b * p.H + h) * p.Lq;
-  const float* dltp = p.delta + ((int64_t)b * p.H + h) * p.Lq;
+  const float* ndltp = p.ndelta + ((int64_t)b * p.H + h) * p.Lq;
 
   Frag kf[NC], vf[NC];
 #pragma unroll
@@ -193,7 +194,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
     if (tid < BQ) {
       const int q = q0 + tid;
       lse_s[tid] = q < p.Lq ? lsep[q] * kLog2e : 0.f;
-      dlt_s[tid] = q < p.Lq ? dltp[q] : 0.f;
+      dlt_s[tid] = q < p.Lq ? -ndltp[q] : 0.f;
     }
     __syncthreads();
 
@@ -328,7 +329,7 @@ __global__ __launch_bounds__(256) void dq_kernel(const Params p) {
   }
   const int64_t rowid = ((int64_t)b * p.H + h) * p.Lq + qclamp;
   const float lse2 = p.lse[rowid] * kLog2e;
-  const float dlt = p.delta[rowid];
+  const float dlt = -p.ndelta[rowid];
 
   f32x16 dq[NDB];
 #pragma unroll

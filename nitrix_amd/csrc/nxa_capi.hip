@@ -168,7 +168,7 @@ WsLayout ws_layout(const nxa_desc* d, int has_bias, int has_mask, int is_bwd) {
     off += align256(mask_geom(d).bytes);
   }
   if (is_bwd) {
-    w.delta = off;  // delta[B*H*Lq], then lse2[B*H*Lq]
+    w.delta = off;  // -delta[B*H*Lq], then -lse2[B*H*Lq]
     off += 2 * align256((size_t)d->B * d->H * d->Lq * sizeof(float));
     if (has_bias) {
       w.partial = off;
@@ -368,8 +368,8 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
   p.dq = dq;
   p.dk = dk;
   p.dv = dv;
-  p.delta = reinterpret_cast<float*>(wsb + ws.delta);
-  p.lse2 = reinterpret_cast<float*>(
+  p.ndelta = reinterpret_cast<float*>(wsb + ws.delta);
+  p.nlse2 = reinterpret_cast<float*>(
       wsb + ws.delta + align256((size_t)d->B * d->H * d->Lq * sizeof(float)));
   if ((rc = launch("delta", stream,
                    [&] { nxa::launch_delta(p, d->io_dtype, stream); })))

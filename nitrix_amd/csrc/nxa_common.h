@@ -63,8 +63,8 @@ struct Params {
   void* dk;
   void* dv;
   void* dbias;         // final dbias, or the fp32 partial buffer (dbias_f32=1)
-  float* delta;        // [B, H, Lq] rowsum(O * dO)        (backward workspace)
-  float* lse2;         // [B, H, Lq] lse * log2(e)          (backward workspace)
+  float* ndelta;       // [B, H, Lq] -rowsum(O * dO)       (backward workspace)
+  float* nlse2;        // [B, H, Lq] -lse * log2(e)         (backward workspace)
   const uint8_t* tilemap;
   uint8_t* tilemap_out;
 
@@ -328,10 +328,19 @@ __device__ __forceinline__ void dma4(const void* g, void* lds) {
                :: "v"(g), "s"(m) : "m0");
 }
 
+// Instruction classes of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedDsRead = 0x100,
+              kSchedDsWrite = 0x200;
+
 // s_waitcnt immediate that waits for vmcnt <= n and leaves expcnt / lgkmcnt
 // unconstrained (gfx9 encoding: vmcnt bits [3:0] and [15:14]).
 __device__ __forceinline__ constexpr int vmcnt_imm(int n) {
   return (n & 0xF) | (((n >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8);
+}
+// s_waitcnt immediate that waits for lgkmcnt <= n (LDS / scalar memory)
+// and leaves vmcnt / expcnt unconstrained.
+__device__ __forceinline__ constexpr int lgkmcnt_imm(int n) {
+  return 0xF | (3 << 14) | (0x7 << 4) | ((n & 0xF) << 8);
 }
 
 // Workgroup barrier without a memory fence: LDS filled by direct copies is
@@ -455,20 +464,50 @@ struct SwzStream {
   __device__ __forceinline__ void issue(const bf16* src, int64_t rs, int r0,
                                         int nrows, int D, uint32_t lds, int wave,
                                         int lane) const {
+#pragma unroll
+    for (int m = 0; m < CNT; ++m) issue_one(src, rs, r0, nrows, D, lds, m, wave, lane);
+  }
+  // Copy m of the wave's CNT copies of that tile.
+  __device__ __forceinline__ void issue_one(const bf16* src, int64_t rs, int r0,
+                                            int nrows, int D, uint32_t lds, int m,
+                                            int wave, int lane) const {
     const bf16* base = src + (int64_t)r0 * rs;  // wave-uniform
     if (r0 + 64 <= nrows) {
-#pragma unroll
-      for (int m = 0; m < CNT; ++m) dma16_sv(base, off[m], lds + (m * NW + wave) * 1024);
+      dma16_sv(base, off[m], lds + (m * NW + wave) * 1024);
     } else {
-#pragma unroll
-      for (int m = 0; m < CNT; ++m) {
-        const int r = min(row_of(m, wave, lane), nrows - 1 - r0);
-        dma16_sv(base, 2u * (uint32_t)(r * rs + col_of(m, wave, lane, D)),
-                 lds + (m * NW + wave) * 1024);
-      }
+      const int r = min(row_of(m, wave, lane), nrows - 1 - r0);
+      dma16_sv(base, 2u * (uint32_t)(r * rs + col_of(m, wave, lane, D)),
+               lds + (m * NW + wave) * 1024);
     }
   }
 };
+
+// Buffer resource (V#) of the raw byte range [base, base + bytes): buffer
+// loads at offsets beyond it return zero instead of touching memory, so a
+// tile that runs past the end of a matrix needs no clamping (and a range of
+// zero bytes turns a copy into a no-op that still counts in vmcnt).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffff));  // stride 0
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+// Direct copies through a buffer resource: 16 (or 4) bytes at byte offset
+// voff of the range to LDS byte offset `lds` (wave-uniform) + 16 (4) * lane.
+__device__ __forceinline__ void dma16_buf(i32x4 rsrc, uint32_t voff, uint32_t lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(voff), "s"(rsrc), "s"(m) : "m0");
+}
+__device__ __forceinline__ void dma4_buf(i32x4 rsrc, uint32_t voff, uint32_t lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
+               :: "v"(voff), "s"(rsrc), "s"(m) : "m0");
+}
 
 // Direct copy of 4 bytes per lane to LDS byte offset `lds` (wave-uniform):
 // lane l's dword lands at lds + 4 l.

@@ -56,8 +56,6 @@ namespace nxa {
 
 constexpr int kFwdMaxTiles = 1024;       // key tiles listed in LDS per block
 constexpr float kFwdRescaleSlack = 8.0f;  // lazy max raise threshold (log2)
-// Instruction classes of __builtin_amdgcn_sched_group_barrier.
-constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedDsRead = 0x100;
 
 // max over the two 32-lane halves (lanes l and l ^ 32).
 __device__ __forceinline__ float half_max(float x) {
