@@ -80,7 +80,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
   constexpr int TILE_BYTES = BQ * DP * 2;
   constexpr int ROWS_OFF = 2 * TILE_BYTES;             // -lse2[64], then -delta[64]
   constexpr int STAGE_BYTES = ROWS_OFF + 2 * BQ * 4;
-  constexpr int PBUF_BYTES = 4 * 2 * 4 * 1024;         // [P wave][query block][quad][lane]
+  constexpr int PB_BYTES = 4 * 2 * 2 * 1024;           // [P wave][query block][frag][lane]
+  constexpr int PBUF_BYTES = 2 * PB_BYTES;             // two P buffers (alternating tiles)
   __shared__ __attribute__((aligned(16))) char smem[NST * STAGE_BYTES + PBUF_BYTES];
   __shared__ uint8_t tcls[kMaxBwdTiles];
   __shared__ int sched_s[4];
@@ -247,15 +248,6 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
     else if (cw < 2)
       dma4_buf(s.r, 4u * lane, at + ROWS_OFF + cw * (BQ * 4));
   };
-  // Waits for all but the latest tile's copies (every tile issues the same
-  // number: NCPY, plus one on waves 4 and 5).
-  auto wait_prev = [&]() NXA_INLINE {
-    if (cw < 2)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(NCPY + 1));
-    else
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(NCPY));
-  };
-
   // --- per-lane LDS read offsets (bytes) --------------------------------------------
   // Row reads (A of S and dP): row c32 of a 32-row block, chunk 2m + g.  The
   // swizzle depends on the row's low 4 bits only, so other blocks and
@@ -276,8 +268,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
     }
   // Per-row values: rows 8c + 4g .. +3 of each 32-row block.
   const uint32_t rvoff = ROWS_OFF + (pw ? 0 : BQ * 4) + 16 * g;
-  // P exchange: the lane's four float4 per query block, 1 KB apart.
-  const uint32_t poff = pbuf + (wave & 3) * (2 * 4 * 1024) + 16 * lane;
+  // P exchange: the lane's two bf16 fragments per query block, 1 KB apart.
+  const uint32_t poff = pbuf + (wave & 3) * (2 * 2 * 1024) + 16 * lane;
 
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
   typedef __attribute__((address_space(3))) Frag lds_frag;
@@ -295,184 +287,202 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
     return r;
   };
 
-  // The tile loop is instantiated per role: identical barrier sequence,
-  // role-specific straight-line bodies.
+  // Row products of one tile: x[qb] = A B^T + (per-row value), A = Q (P
+  // wave) or dO (dS wave) of the tile in stage `at`, two 32-query blocks.
+  // `between(j)` runs after product j (the dS wave's tile copies).
+  auto row_products = [&](uint32_t at, f32x16 (&x)[2], auto&& between) NXA_INLINE {
+    const uint32_t rt = at + (pw ? 0 : TILE_BYTES);
+    uint32_t ra[NC];
+#pragma unroll
+    for (int m = 0; m < NC; ++m) ra[m] = vadd(rt, roff[m]);
+    const uint32_t rv = vadd(at, rvoff);
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const f32x4 v4 = *(const lds_f32x4*)(uintptr_t)(rv + (qb * 32 + 8 * c) * 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[qb][4 * c + j] = v4[j];
+      }
+    // Product j: query block j & 1, head-dim chunk pair j >> 1.  The A
+    // fragments are read PD products ahead (a rotating register buffer) so
+    // the LDS latency is covered.
+    constexpr int NPA = 2 * NC, PD = NPA < 8 ? NPA : 8;
+    auto afrag = [&](int j) NXA_INLINE -> Frag {
+      return *(const lds_frag*)(uintptr_t)(ra[j >> 1] + (j & 1) * (32 * DP * 2));
+    };
+    Frag abuf[PD];
+#pragma unroll
+    for (int j = 0; j < PD; ++j) abuf[j] = afrag(j);
+#pragma unroll
+    for (int j = 0; j < NPA; ++j) {
+      M::run(x[j & 1], abuf[j % PD], bfr[j >> 1]);
+      if (j + PD < NPA) abuf[j % PD] = afrag(j + PD);
+      between(j);
+    }
+    // Keep that order: the row values, PD reads, then one product and one
+    // read at a time.
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8 + PD, 0);
+#pragma unroll
+    for (int j = 0; j < NPA; ++j) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      if (j + PD < NPA) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+  };
+  // Transposed products: acc += A^T F[qb] for both query blocks, A = dO (P
+  // wave) or Q (dS wave) of the tile in stage `at`.
+  auto tr_products = [&](uint32_t at, const Frag (&pf)[2][FPB]) NXA_INLINE {
+    const uint32_t tt = at + (pw ? TILE_BYTES : 0);
+    uint32_t ta[NDB][2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      ta[db][0] = vadd(tt, toff[db][0]);
+      ta[db][1] = vadd(tt, toff[db][1]);
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int f = 0; f < FPB; ++f) {
+        const uint32_t ro = (qb * 32 + 16 * f) * (DP * 2);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          M::run(acc[db], tr_frag(ta[db][0] + ro, ta[db][1] + ro), pf[qb][f]);
+      }
+  };
+
+  // P wave, tile t in stage st: P = exp2(S'), published (bf16) in P buffer
+  // `par`, then dV^T += dO^T P.
+  auto p_tile = [&](int t, int st, int par) NXA_INLINE {
+    const uint32_t at = lds0 + st * STAGE_BYTES;
+    const int q0 = t * BQ;
+    __builtin_amdgcn_s_setprio(DKDV_PRIO);  // the exp pass depends on these
+    f32x16 x[2];
+    row_products(at, x, [](int) {});
+    __builtin_amdgcn_s_setprio(0);
+    const int cls = ucls >= 0 ? ucls : tclass(t);
+    const bool need_mask = mask_rows && !(cls & 2);
+    const bool tail = q0 + BQ > p.Lq;
+    const bool diag = CAUSAL && (kw0 + 31 > q0);
+    const bool general = need_mask || tail || diag || bias_rows;
+    Frag pf[2][FPB];
+    // P of query block qb; GEN selects the element-wise pass (per-row mask,
+    // query tail, causal diagonal, per-row bias) and ADD the per-key term,
+    // so interior tiles run straight-line.
+    auto p_block = [&](int qb, auto gen_tag, auto add_tag) NXA_INLINE {
+      constexpr bool GEN = decltype(gen_tag)::value;
+      constexpr bool ADD = decltype(add_tag)::value;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float xv = x[qb][r];
+        if constexpr (ADD) xv += kadd;
+        if constexpr (GEN) {
+          const int q = q0 + qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          const int qcl = q < p.Lq ? q : p.Lq - 1;
+          if constexpr (HAS_BIAS)
+            if (bias_rows)
+              xv = __builtin_fmaf(load_bias1(p, bbase + (int64_t)qcl * p.bias_str[2]),
+                                  kLog2e, xv);
+          bool keep = q < p.Lq;
+          if (need_mask) keep = keep && mbase[(int64_t)qcl * p.mask_str[2]] != 0;
+          if (CAUSAL) keep = keep && key <= q;
+          xv = keep ? xv : -INFINITY;
+        }
+        x[qb][r] = fast_exp2(xv);
+      }
+#pragma unroll
+      for (int f = 0; f < FPB; ++f) {
+        pf[qb][f] = M::pack(x[qb], f);
+        *(lds_frag*)(uintptr_t)(poff + par * PB_BYTES + (qb * FPB + f) * 1024) = pf[qb][f];
+      }
+    };
+    if (general) {
+      p_block(0, std::true_type{}, std::true_type{});
+      p_block(1, std::true_type{}, std::true_type{});
+    } else if (use_kadd) {
+      p_block(0, std::false_type{}, std::true_type{});
+      p_block(1, std::false_type{}, std::true_type{});
+    } else {
+      p_block(0, std::false_type{}, std::false_type{});
+      p_block(1, std::false_type{}, std::false_type{});
+    }
+    tr_products(at, pf);
+  };
+
+  // dS wave, tile t in stage st (P from buffer `par`): dP - delta, dS, dK^T
+  // += Q^T dS (and dbias); the copies of the next tile (sources s, stage
+  // stn) ride along with the row products.
+  auto ds_tile = [&](int t, int st, int par, const TileSrc& s, int stn) NXA_INLINE {
+    const uint32_t at = lds0 + st * STAGE_BYTES;
+    const int q0 = t * BQ;
+    f32x16 x[2];
+    row_products(at, x, [&](int j) NXA_INLINE {
+      if (j & 1) copy(s, stn, j >> 1);
+    });
+    __builtin_amdgcn_s_setprio(DKDV_PRIO);  // dS and dK form the longer chain
+    Frag pf[2][FPB];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+      for (int f = 0; f < FPB; ++f) {
+        const Frag pb = *(const lds_frag*)(uintptr_t)(poff + par * PB_BYTES + (qb * FPB + f) * 1024);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int r = 8 * f + e;
+          const float ds = (float)pb[e] * x[qb][r];
+          x[qb][r] = ds;
+          if constexpr (DBM == kDbFull) {
+            const int q = q0 + qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (kok && q < p.Lq) store_db(p, dbbase + (int64_t)q * p.dbias_str[2], ds);
+          }
+          if constexpr (DBM == kDbColsum) colsum += ds;
+        }
+        pf[qb][f] = M::pack(x[qb], f);
+      }
+    }
+    tr_products(at, pf);
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  // The tile loop is instantiated per role with the same barrier sequence.
+  // Iteration i: the P wave handles active tile i, the dS wave tile i - 1
+  // (whose P the barrier between them published), and the dS waves copy
+  // tile i + 1 into the stage that tile i - 2 left.
   auto run = [&](auto role_tag) {
     constexpr bool PW = decltype(role_tag)::value;
-    int cur = next_active(0);
-    int nxt = cur < nq ? next_active(cur + 1) : nq;
+    int cur = next_active(0), prv = nq;
+    int stc = 0, stp = 2, par = 0;
     if constexpr (!PW) {
-      const TileSrc s0 = tile_src(cur), s1 = tile_src(nxt);
+      const TileSrc s0 = tile_src(cur);
 #pragma unroll
       for (int j = 0; j <= NCPY; ++j) copy(s0, 0, j);
-#pragma unroll
-      for (int j = 0; j <= NCPY; ++j) copy(s1, 1, j);
-      wait_prev();
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     }
     barrier_nofence();
-    int st = 0;
-
-    while (cur < nq) {
-      const int nxt2 = nxt < nq ? next_active(nxt + 1) : nq;
-      const int st2 = st == 0 ? 2 : st - 1;  // stage of tile cur - 1, free now
-      TileSrc s2;
-      if constexpr (!PW) {
-        s2 = tile_src(nxt2);
-        copy(s2, st2, NCPY);
-      }
-
-      const uint32_t at = lds0 + st * STAGE_BYTES;
-      const int q0 = cur * BQ;
-      // A operand of the row products: Q (P wave) or dO (dS wave); of the
-      // transposed products: dO (P wave) or Q (dS wave).
-      const uint32_t rt = at + (PW ? 0 : TILE_BYTES);
-      const uint32_t tt = at + (PW ? TILE_BYTES : 0);
-      uint32_t ra[NC];
-#pragma unroll
-      for (int m = 0; m < NC; ++m) ra[m] = vadd(rt, roff[m]);
-      const uint32_t rv = vadd(at, rvoff);
-
-      // Phase A: X = A B^T - row value, two 32-query blocks.  The P wave's
-      // products go first (its exp pass depends on them).
-      if constexpr (PW) __builtin_amdgcn_s_setprio(DKDV_PRIO);
-      f32x16 x[2];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const f32x4 v4 = *(const lds_f32x4*)(uintptr_t)(rv + (qb * 32 + 8 * c) * 4);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) x[qb][4 * c + j] = v4[j];
-        }
-      // Product j: query block j & 1, head-dim chunk pair j >> 1.  The A
-      // fragments are read PD products ahead (a rotating register buffer)
-      // so the LDS latency is covered.
-      constexpr int NPA = 2 * NC, PD = NPA < 8 ? NPA : 8;
-      auto afrag = [&](int j) NXA_INLINE -> Frag {
-        return *(const lds_frag*)(uintptr_t)(ra[j >> 1] + (j & 1) * (32 * DP * 2));
-      };
-      Frag abuf[PD];
-#pragma unroll
-      for (int j = 0; j < PD; ++j) abuf[j] = afrag(j);
-#pragma unroll
-      for (int j = 0; j < NPA; ++j) {
-        M::run(x[j & 1], abuf[j % PD], bfr[j >> 1]);
-        if (j + PD < NPA) abuf[j % PD] = afrag(j + PD);
-        // dS wave: one tile copy after every second product.
-        if constexpr (!PW)
-          if (j & 1) copy(s2, st2, j >> 1);
-      }
-      // Keep that order: the row values, PD reads, then one product and one
-      // read at a time.
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8 + PD, 0);
-#pragma unroll
-      for (int j = 0; j < NPA; ++j) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        if (j + PD < NPA) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      }
-
-      Frag pf[2][FPB];  // P (P wave) or dS (dS wave) as reduction fragments
+    while (cur < nq || prv < nq) {
+      const int nxt = cur < nq ? next_active(cur + 1) : nq;
+      const int stn = stc == 2 ? 0 : stc + 1;
       if constexpr (PW) {
-        const int cls = ucls >= 0 ? ucls : tclass(cur);
-        const bool need_mask = mask_rows && !(cls & 2);
-        const bool tail = q0 + BQ > p.Lq;
-        const bool diag = CAUSAL && (kw0 + 31 > q0);
-        const bool general = need_mask || tail || diag || bias_rows;
-        // P of query block qb; GEN selects the element-wise pass (per-row
-        // mask, query tail, causal diagonal, per-row bias) and ADD the
-        // per-key term, so interior tiles run straight-line.
-        auto p_block = [&](int qb, auto gen_tag, auto add_tag) NXA_INLINE {
-          constexpr bool GEN = decltype(gen_tag)::value;
-          constexpr bool ADD = decltype(add_tag)::value;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float xv = x[qb][r];
-            if constexpr (ADD) xv += kadd;
-            if constexpr (GEN) {
-              const int q = q0 + qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-              const int qcl = q < p.Lq ? q : p.Lq - 1;
-              if constexpr (HAS_BIAS)
-                if (bias_rows)
-                  xv = __builtin_fmaf(
-                      load_bias1(p, bbase + (int64_t)qcl * p.bias_str[2]), kLog2e, xv);
-              bool keep = q < p.Lq;
-              if (need_mask) keep = keep && mbase[(int64_t)qcl * p.mask_str[2]] != 0;
-              if (CAUSAL) keep = keep && key <= q;
-              xv = keep ? xv : -INFINITY;
-            }
-            x[qb][r] = fast_exp2(xv);
-          }
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            *(lds_f32x4*)(uintptr_t)(poff + (qb * 4 + c) * 1024) =
-                f32x4{x[qb][4 * c], x[qb][4 * c + 1], x[qb][4 * c + 2], x[qb][4 * c + 3]};
-#pragma unroll
-          for (int f = 0; f < FPB; ++f) pf[qb][f] = M::pack(x[qb], f);
-        };
-        if (general) {
-          p_block(0, std::true_type{}, std::true_type{});
-          p_block(1, std::true_type{}, std::true_type{});
-        } else if (use_kadd) {
-          p_block(0, std::false_type{}, std::true_type{});
-          p_block(1, std::false_type{}, std::true_type{});
-        } else {
-          p_block(0, std::false_type{}, std::false_type{});
-          p_block(1, std::false_type{}, std::false_type{});
-        }
-        // P is in LDS before the phase barrier.
+        if (cur < nq) p_tile(cur, stc, par);
+        // P is in LDS before the barrier.
         __builtin_amdgcn_s_waitcnt(lgkmcnt_imm(0));
-        __builtin_amdgcn_s_setprio(0);
+      } else {
+        const TileSrc s = tile_src(nxt);
+        copy(s, stn, NCPY);
+        if (prv < nq) {
+          ds_tile(prv, stp, par ^ 1, s, stn);
+        } else {
+#pragma unroll
+          for (int j = 0; j < NCPY; ++j) copy(s, stn, j);
+        }
+        // Tile nxt is resident before the barrier.
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       }
       barrier_nofence();
-
-      // Phase B: acc += A^T F (F = P or dS); the dS wave's chain (read P,
-      // dS, products) goes first.
-      if constexpr (!PW) __builtin_amdgcn_s_setprio(DKDV_PRIO);
-      uint32_t ta[NDB][2];
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        ta[db][0] = vadd(tt, toff[db][0]);
-        ta[db][1] = vadd(tt, toff[db][1]);
-      }
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        if constexpr (!PW) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const f32x4 p4 = *(const lds_f32x4*)(uintptr_t)(poff + (qb * 4 + c) * 1024);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int r = 4 * c + j;
-              const float ds = p4[j] * x[qb][r];
-              x[qb][r] = ds;
-              if constexpr (DBM == kDbFull) {
-                const int q = q0 + qb * 32 + 8 * c + 4 * g + j;
-                if (kok && q < p.Lq) store_db(p, dbbase + (int64_t)q * p.dbias_str[2], ds);
-              }
-              if constexpr (DBM == kDbColsum) colsum += ds;
-            }
-          }
-#pragma unroll
-          for (int f = 0; f < FPB; ++f) pf[qb][f] = M::pack(x[qb], f);
-        }
-#pragma unroll
-        for (int f = 0; f < FPB; ++f) {
-          const uint32_t ro = (qb * 32 + 16 * f) * (DP * 2);
-#pragma unroll
-          for (int db = 0; db < NDB; ++db)
-            M::run(acc[db], tr_frag(ta[db][0] + ro, ta[db][1] + ro), pf[qb][f]);
-        }
-      }
-
-      // Tile nxt must be resident before the barrier; nxt2 may stay in flight.
-      if constexpr (!PW) {
-        __builtin_amdgcn_s_setprio(0);
-        wait_prev();
-      }
-      barrier_nofence();
-      st = st == 2 ? 0 : st + 1;
+      prv = cur;
+      stp = stc;
       cur = nxt;
-      nxt = nxt2;
+      stc = stn;
+      par ^= 1;
     }
   };
   if (pw)
