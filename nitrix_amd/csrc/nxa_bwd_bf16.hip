@@ -520,33 +520,43 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ.  Block = 4 waves x 32 queries (128); streams 64-key tiles in two
-// 32-key halves.  S^T = K Q^T and dP^T = V dO^T put the query on the lane's
-// column, so dS^T feeds dQ^T = K^T dS^T from registers; K^T is read
-// transposed from the row-major K tile.  K / V tiles arrive by direct
-// global->LDS copies into a double-buffered ring (no staging registers), one
-// tile ahead; two blocks share a CU.
+// dQ.  Block = 4 waves x 32 queries (128); two blocks share a CU.  Each wave
+// holds its queries' Q and dO rows stationary and streams 64-key tiles:
+// S^T = K Q^T and dP^T = V dO^T put the query on the lane's column, so dS^T
+// feeds dQ^T += K^T dS^T from registers; K^T comes from ds_read_b64_tr_b16
+// reads of the row-major (swizzled) K tile.  K / V tiles reach an LDS ring
+// by direct copies through buffer resources bounded at Lk (keys past it
+// read as zero and are masked), one tile ahead at D = 128 and two at D = 64,
+// each wave copying its share between its S / dP products.  A bias that
+// broadcasts over queries (BMODE kFbRow) enters S^T through one more MFMA
+// per 32-key block, as in the forward; other biases take the element pass.
 // ---------------------------------------------------------------------------
-template <int DP, bool HAS_BIAS, bool CAUSAL>
+template <int DP, int BMODE, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
   using M = Mma<bf16>;
   using Frag = bf16x8;
   constexpr int EPC = 8, KC = 16;
-  constexpr int BM = 128, BN = 64;
-  constexpr int TSZ = BN * DP;         // swizzled, unpadded tile (elements)
-  constexpr int NC = DP / KC, NDB = DP / 32;
-  constexpr int FPB = M::FRAGS_PER_BLOCK;
-  constexpr int CPRW = DP / 8;
-  constexpr int RPB = 64 / CPRW;
-  constexpr int BPW = TSZ / 512 / 4;
-  __shared__ __attribute__((aligned(16))) bf16 tiles[2][2][TSZ];  // [stage][K|V]
-  __shared__ uint8_t tcls[kMaxBwdTiles];
+  constexpr int NW = 4, BM = NW * 32, BN = 64;
+  constexpr int NC = DP / KC, NDB = DP / 32, FPB = M::FRAGS_PER_BLOCK;
+  constexpr bool ROW_BIAS = BMODE == kFbRow;
+  constexpr bool VALU_BIAS = BMODE == kFbValu;
+  using KS = SwzStream<DP, NW>;
+  constexpr int TILE_BYTES = BN * DP * 2;
+  constexpr int ROWB_BYTES = ROW_BIAS ? NW * 256 : 0;  // each wave's copy of the bias row
+  constexpr int STAGE_BYTES = 2 * TILE_BYTES + ROWB_BYTES;
+  constexpr int NST = DP == 64 ? 3 : 2;                // K / V stages (two blocks per CU)
+  constexpr int CPT = 2 * KS::CNT + (ROW_BIAS ? 1 : 0);  // copies per wave per tile
+  __shared__ __attribute__((aligned(16))) char smem[NST * STAGE_BYTES];
+  __shared__ uint16_t act[kMaxBwdTiles];  // active key tiles, in order
+  __shared__ uint8_t acls[kMaxBwdTiles];  // their classes
+  __shared__ int nact_s;
 
   const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
   const int bh = vid / p.nqt;
-  const int qt = p.nqt - 1 - (vid % p.nqt);
+  const int qt = p.nqt - 1 - (vid % p.nqt);  // longest (causal) blocks first
   const int b = bh / p.H, h = bh % p.H;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
   const int g = lane >> 5, c32 = lane & 31;
   const int q0 = qt * BM;
   const int qw0 = q0 + wave * 32;
@@ -558,23 +568,41 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
   const bf16* vp = (const bf16*)p.v + b * p.v_str[0] + h * p.v_str[1];
   const int64_t ks = p.k_str[2], vs = p.v_str[2];
 
+  // --- active key tiles of this block (tile-map classes) --------------------
   const int k_end = CAUSAL ? min(p.Lk, q0 + BM) : p.Lk;
   const int nkt = (k_end + BN - 1) / BN;
-  const bool cls_lds = p.has_tilemap && nkt <= kMaxBwdTiles;
-  if (cls_lds)
-    for (int t = tid; t < nkt; t += 256)
-      tcls[t] = (uint8_t)tile_class(p, b, h, q0, q0 + BM, t * BN, t * BN + BN);
-  __syncthreads();
-  auto tclass = [&](int t) -> int {
-    if (!p.has_tilemap) return 3;
-    if (cls_lds) return tcls[t];
-    return tile_class(p, b, h, q0, q0 + BM, t * BN, t * BN + BN);
+  const bool listed = p.has_tilemap && nkt <= kMaxBwdTiles;
+  auto class_g = [&](int t) -> int {
+    return p.has_tilemap ? tile_class(p, b, h, q0, q0 + BM, t * BN, t * BN + BN) : 3;
   };
-  auto next_active = [&](int t) {
-    while (t < nkt && !(tclass(t) & 1)) ++t;
-    return t;
+  if (listed && wave == 0) {
+    int base = 0;
+    for (int t0 = 0; t0 < nkt; t0 += 64) {
+      const int t = t0 + lane;
+      const int c = t < nkt ? class_g(t) : 0;
+      const uint64_t m = __ballot(c & 1);
+      if (c & 1) {
+        const int pos = base + __popcll(m & ((1ull << lane) - 1));
+        act[pos] = (uint16_t)t;
+        acls[pos] = (uint8_t)c;
+      }
+      base += __popcll(m);
+    }
+    if (lane == 0) nact_s = base;
+  }
+  __syncthreads();
+  const int n = listed ? __builtin_amdgcn_readfirstlane(nact_s) : nkt;
+  // Contiguous active tiles (no mask, key padding, causal) need no lookup.
+  const bool dense = !listed || n == 0 || act[n - 1] == n - 1;
+  auto tile_of = [&](int i) NXA_INLINE -> int {
+    return dense ? i : __builtin_amdgcn_readfirstlane((int)act[i]);
+  };
+  auto class_of = [&](int i) NXA_INLINE -> int {
+    if (!p.has_tilemap) return 3;
+    return listed ? __builtin_amdgcn_readfirstlane((int)acls[i]) : class_g(tile_of(i));
   };
 
+  // --- stationary Q^T, dO^T fragments and per-row values ------------------------
   Frag qf[NC], df[NC];
   {
     const bf16* qp = (const bf16*)p.q + b * p.q_str[0] + h * p.q_str[1] +
@@ -591,16 +619,23 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
   }
   const int64_t rowid = ((int64_t)b * p.H + h) * p.Lq + qc;
   const float neg_lse2 = p.nlse2[rowid];
-  const float dlt = -p.ndelta[rowid];
-  const int64_t brow = HAS_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] +
-                                      (int64_t)qc * p.bias_str[2]
-                                : 0;
+  const float ndlt = p.ndelta[rowid];
+  const int64_t brow = VALU_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] +
+                                       (int64_t)qc * p.bias_str[2]
+                                 : 0;
   const uint8_t* mrow = p.has_mask ? p.mask + b * p.mask_str[0] +
                                          h * p.mask_str[1] +
                                          (int64_t)qc * p.mask_str[2]
                                    : nullptr;
-  // Stationary loads complete before the copies start (vmcnt in the loop
-  // then only tracks tile copies).
+  // Row bias: B[0][q] = h (or l) for every query, reduction row 0 only.
+  Frag bdh = zero_frag<bf16>(), bdl = zero_frag<bf16>();
+  if constexpr (ROW_BIAS) {
+    bdh[0] = (bf16)(g == 0 ? p.bias_h : 0.f);
+    bdl[0] = (bf16)(g == 0 ? p.bias_l : 0.f);
+  }
+  const bool bias_l = ROW_BIAS && p.bias_l != 0.f;  // uniform
+  // The stationary loads complete here, so the waits in the tile loop only
+  // count tile copies.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   f32x16 dq[NDB];
@@ -609,93 +644,226 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
 
-  // Copies of key tile t into ring stage st (rows past Lk clamped to the last
-  // key, head-dim chunks past D to chunk 0; both are masked or cancelled).
-  auto issue = [&](int t, int st) {
-    const int k0 = t * BN;
-#pragma unroll
-    for (int i = 0; i < BPW; ++i) {
-      const int blk = wave * BPW + i;
-      const int row = blk * RPB + lane / CPRW;
-      const int lc = (lane % CPRW) ^ swz<DP>(row);
-      const int key = min(k0 + row, p.Lk - 1);
-      const int col = lc * 8 < p.D ? lc * 8 : 0;
-      dma16(kp + (int64_t)key * ks + col, &tiles[st][0][blk * 512]);
-      dma16(vp + (int64_t)key * vs + col, &tiles[st][1][blk * 512]);
-    }
+  // --- copies --------------------------------------------------------------------
+  KS ksm, vsm;
+  ksm.init(ks, p.D, wave, lane);
+  vsm.init(vs, p.D, wave, lane);
+  const uint32_t lds0 = lds_offset(smem);
+  const bf16* bp = ROW_BIAS ? (const bf16*)p.bias + b * p.bias_str[0] + h * p.bias_str[1]
+                            : nullptr;
+  struct TileSrc {
+    i32x4 k, v, r;  // K rows, V rows, bias row
+  };
+  // Sources of active tile i (an empty range past the last one, so every
+  // tile issues the same copies).
+  auto tile_src = [&](int i) NXA_INLINE -> TileSrc {
+    const int k0 = i < n ? tile_of(i) * BN : p.Lk;
+    const int left = p.Lk - k0;
+    TileSrc s;
+    s.k = make_rsrc(kp + (int64_t)k0 * ks,
+                    left > 0 ? (uint32_t)(((int64_t)(left - 1) * ks + p.D) * 2) : 0u);
+    s.v = make_rsrc(vp + (int64_t)k0 * vs,
+                    left > 0 ? (uint32_t)(((int64_t)(left - 1) * vs + p.D) * 2) : 0u);
+    if constexpr (ROW_BIAS)
+      s.r = make_rsrc(bp + k0, (uint32_t)max(left, 0) * 2u);
+    return s;
+  };
+  // Copy j of a tile into stage st: K share, V share, then the bias row
+  // (lane l: keys 2(l % 32), 2(l % 32) + 1, so the row lands twice).
+  auto copy = [&](const TileSrc& s, int st, int j) NXA_INLINE {
+    const uint32_t at = lds0 + st * STAGE_BYTES;
+    if (j < KS::CNT)
+      dma16_buf(s.k, ksm.off[j], at + (j * NW + wave) * 1024);
+    else if (j < 2 * KS::CNT)
+      dma16_buf(s.v, vsm.off[j - KS::CNT], at + TILE_BYTES + ((j - KS::CNT) * NW + wave) * 1024);
+    else if (ROW_BIAS)
+      dma4_buf(s.r, 4u * c32, at + 2 * TILE_BYTES + wave * 256);
   };
 
-  int kt = next_active(0);
-  if (kt < nkt) issue(kt, 0);
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  // --- per-lane LDS read offsets (bytes) ----------------------------------------
+  uint32_t koff[NC];  // row reads: row c32 of a 32-key block, chunk 2m + g
+#pragma unroll
+  for (int m = 0; m < NC; ++m) koff[m] = 2 * swz_off<DP>(c32, 2 * m + g);
+  const int tr_row = 4 * ((lane >> 4) >> 1) + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  uint32_t toff[NDB][2];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int col = db * 32 + tr_col;
+      toff[db][hh] = 2 * (swz_off<DP>(tr_row + 8 * hh, col >> 3) + (col & 7));
+    }
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  typedef __attribute__((address_space(3))) Frag lds_frag;
+  typedef __attribute__((address_space(3))) bf16 lds_bf16;
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  auto tr_frag = [&](uint32_t a0, uint32_t a1) NXA_INLINE -> Frag {
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a0);
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a1);
+    const i16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(Frag, r);
+  };
+  auto vadd = [](uint32_t sb, uint32_t v) NXA_INLINE -> uint32_t {
+    uint32_t r;
+    asm("v_add_u32 %0, %1, %2" : "=v"(r) : "s"(sb), "v"(v));
+    return r;
+  };
+
+  // --- tile loop ----------------------------------------------------------------
+  // Tile i lives in stage i % NST; after the barrier that starts tile i the
+  // stage of tile i - 1 is free and receives tile i + NST - 1.
+  {
+    TileSrc s0 = tile_src(0);
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) copy(s0, 0, j);
+    if constexpr (NST > 2) {
+      TileSrc s1 = tile_src(1);
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) copy(s1, 1, j);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(CPT));
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+  }
   barrier_nofence();
-  int st = 0;
 
-  while (kt < nkt) {
-    const int cls = tclass(kt);
-    const int kn = next_active(kt + 1);
-    if (kn < nkt) issue(kn, st ^ 1);
+  for (int i = 0; i < n; ++i) {
+    const int st = i % NST;
+    const int stn = (i + NST - 1) % NST;
+    const TileSrc sn = tile_src(i + NST - 1);
+    const uint32_t at = lds0 + st * STAGE_BYTES;
+    const int k0 = tile_of(i) * BN;
 
-    const bf16* Ks = tiles[st][0];
-    const bf16* Vs = tiles[st][1];
-    const int k0 = kt * BN;
+    const int cls = class_of(i);
     const bool need_mask = p.has_mask && !(cls & 2);
     const bool tail = k0 + BN > p.Lk;
     const bool diag = CAUSAL && (k0 + BN - 1 > qw0);
+    const bool general = VALU_BIAS || need_mask || tail || diag;
+    uint32_t ka[NC];
+#pragma unroll
+    for (int m = 0; m < NC; ++m) ka[m] = vadd(at, koff[m]);
+    uint32_t ta[NDB][2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      ta[db][0] = vadd(at, toff[db][0]);
+      ta[db][1] = vadd(at, toff[db][1]);
+    }
 
-    const bool general = HAS_BIAS || need_mask || tail || diag;
+    // Two 32-key blocks, one after the other.
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      f32x16 s, dpt;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = 0.f;
-        dpt[r] = 0.f;
+      // S^T (+ row bias) and dP^T: product j is S chunk j / 2 (j even) or
+      // dP chunk j / 2 (j odd); A fragments are read PD products ahead, and
+      // this wave's copies of tile i + NST - 1 ride along (one per four
+      // products).
+      f32x16 s, dp;
+      bool fresh = true;
+      if constexpr (ROW_BIAS) {
+        const uint32_t rb = at + 2 * TILE_BYTES + wave * 256;
+        Frag a = zero_frag<bf16>();
+        const bf16 bv = *(const lds_bf16*)(uintptr_t)(rb + 2 * (kb * 32 + c32));
+        a[0] = g == 0 ? bv : (bf16)0.f;
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bdh, f32x16{}, 0, 0, 0);
+        if (bias_l) M::run(s, a, bdl);
+        fresh = false;
       }
+      constexpr int NP = 2 * NC, PD = (DP == 128 && ROW_BIAS) ? 4 : 8;
+      auto afrag = [&](int j) NXA_INLINE -> Frag {
+        const uint32_t base = ka[j >> 1] + ((j & 1) ? TILE_BYTES : 0);
+        return *(const lds_frag*)(uintptr_t)(base + kb * (32 * DP * 2));
+      };
+      Frag abuf[PD];
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int off = swz_off<DP>(kb * 32 + c32, 2 * c + g);
-        M::run(s, ld16(&Ks[off]), qf[c]);
-        M::run(dpt, ld16(&Vs[off]), df[c]);
-      }
+      for (int j = 0; j < PD; ++j) abuf[j] = afrag(j);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int key0 = k0 + kb * 32 + 8 * c + 4 * g;
-        f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-        uint32_t mw = 0x01010101u;
-        if (general) {
-          if constexpr (HAS_BIAS) bv = load_bias4(p, p.bias, brow + key0, p.Lk - key0);
-          if (need_mask) mw = load_mask4(p, mrow + key0, p.Lk - key0);
+      for (int j = 0; j < NP; ++j) {
+        const int m = j >> 1;
+        if (j & 1) {
+          if (j == 1)
+            dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(abuf[j % PD], df[m], f32x16{}, 0, 0, 0);
+          else
+            M::run(dp, abuf[j % PD], df[m]);
+        } else {
+          if (fresh && j == 0)
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(abuf[j % PD], qf[m], f32x16{}, 0, 0, 0);
+          else
+            M::run(s, abuf[j % PD], qf[m]);
         }
+        if (j + PD < NP) abuf[j % PD] = afrag(j + PD);
+        const int pc = kb * NP + j;  // product count in this tile
+        if ((pc & 3) == 3 && (pc >> 2) < CPT) copy(sn, stn, pc >> 2);
+      }
+      if (kb == 1) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = 4 * c + j;
-          float x = __builtin_fmaf(s[r], p.scale_log2, neg_lse2);
-          if (general) {
-            const int kk = key0 + j;
-            if constexpr (HAS_BIAS) x = __builtin_fmaf(bv[j], kLog2e, x);
-            bool keep = mask_bit(mw, j) && kk < p.Lk && qok;
-            if (CAUSAL) keep = keep && kk <= qrow;
-            x = keep ? x : -INFINITY;
+        for (int jc = NP / 2; jc < CPT; ++jc) copy(sn, stn, jc);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, PD, 0);
+#pragma unroll
+      for (int j = 0; j < NP; ++j) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        if (j + PD < NP) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+
+      // dS^T = P (dP - delta), P = exp2(S c - lse2) (+ element pass).
+      Frag pd[FPB];
+      auto ds_block = [&](auto gen_tag) NXA_INLINE {
+        constexpr bool GEN = decltype(gen_tag)::value;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int key0 = k0 + kb * 32 + 8 * c + 4 * g;
+          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+          uint32_t mw = 0x01010101u;
+          if constexpr (GEN) {
+            if constexpr (VALU_BIAS) bv = load_bias4(p, p.bias, brow + key0, p.Lk - key0);
+            if (need_mask) mw = load_mask4(p, mrow + key0, p.Lk - key0);
           }
-          const float pr = fast_exp2(x);
-          dpt[r] = pr * (dpt[r] - dlt);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * c + j;
+            float x = __builtin_fmaf(s[r], p.scale_log2, neg_lse2);
+            if constexpr (GEN) {
+              const int kk = key0 + j;
+              if constexpr (VALU_BIAS) x = __builtin_fmaf(bv[j], kLog2e, x);
+              bool keep = mask_bit(mw, j) && kk < p.Lk && qok;
+              if (CAUSAL) keep = keep && kk <= qrow;
+              x = keep ? x : -INFINITY;
+            }
+            dp[r] = fast_exp2(x) * (dp[r] + ndlt);
+          }
         }
-      }
 #pragma unroll
-      for (int f = 0; f < FPB; ++f) {
-        const Frag pd = M::pack(dpt, f);
+        for (int f = 0; f < FPB; ++f) pd[f] = M::pack(dp, f);
+      };
+      if (general)
+        ds_block(std::true_type{});
+      else
+        ds_block(std::false_type{});
+
+      // dQ^T += K^T dS^T.
+      constexpr int NQ = FPB * NDB, PQ = NQ < 4 ? NQ : 4;
+      auto kfrag = [&](int j) NXA_INLINE -> Frag {
+        const int f = j / NDB, db = j % NDB;
+        const uint32_t ro = (kb * 32 + 16 * f) * (DP * 2);
+        return tr_frag(ta[db][0] + ro, ta[db][1] + ro);
+      };
+      Frag kbuf[PQ];
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
-          M::run(dq[db], lds_tr_frag_swz<DP>(Ks, kb * 32, db * 32, lane, f), pd);
+      for (int j = 0; j < PQ; ++j) kbuf[j] = kfrag(j);
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        M::run(dq[j % NDB], kbuf[j % PQ], pd[j / NDB]);
+        if (j + PQ < NQ) kbuf[j % PQ] = kfrag(j + PQ);
       }
     }
 
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // tile kn resident
+    // Tile i + 1 is resident before the barrier (later tiles may stay in
+    // flight).
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(CPT * (NST - 2)));
     barrier_nofence();
-    st ^= 1;
-    kt = kn;
   }
+  // No copy may still be writing LDS when the block ends.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   if (qok) {
     bf16* dqp = (bf16*)p.dq + b * p.q_str[0] + h * p.q_str[1] + (int64_t)qrow * p.q_str[2];
@@ -743,22 +911,26 @@ void launch_dkdv_bf16(const Params& p, int dp, hipStream_t stream) {
   }
 }
 
-template <int DP, bool HB, bool CA>
+template <int DP, int BMODE, bool CA>
 static void launch_dq_bf16_t(Params p, hipStream_t stream) {
   p.nqt = (p.Lq + 127) / 128;
   const int n = p.B * p.H * p.nqt;
-  hipLaunchKernelGGL((dq_bf16_kernel<DP, HB, CA>), dim3(n), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((dq_bf16_kernel<DP, BMODE, CA>), dim3(n), dim3(256), 0, stream, p);
 }
 
+template <int DP, int BMODE>
+static void launch_dq_bf16_c(const Params& p, hipStream_t stream) {
+  if (p.causal) launch_dq_bf16_t<DP, BMODE, true>(p, stream);
+  else launch_dq_bf16_t<DP, BMODE, false>(p, stream);
+}
+
+// Bias: through an MFMA when it broadcasts over queries (the forward's row
+// mode), else the element pass.
 template <int DP>
 static void launch_dq_bf16_flags(const Params& p, hipStream_t stream) {
-  if (p.has_bias) {
-    if (p.causal) launch_dq_bf16_t<DP, true, true>(p, stream);
-    else launch_dq_bf16_t<DP, true, false>(p, stream);
-  } else {
-    if (p.causal) launch_dq_bf16_t<DP, false, true>(p, stream);
-    else launch_dq_bf16_t<DP, false, false>(p, stream);
-  }
+  if (!p.has_bias) launch_dq_bf16_c<DP, kFbNone>(p, stream);
+  else if (p.fwd_bias == kFbRow) launch_dq_bf16_c<DP, kFbRow>(p, stream);
+  else launch_dq_bf16_c<DP, kFbValu>(p, stream);
 }
 
 void launch_dq_bf16(const Params& p, int dp, hipStream_t stream) {
