@@ -8,16 +8,16 @@
 // and streams key tiles.
 //
 // Layout choices for CDNA4:
-// * streamed tiles stay row-major in LDS; the transposed operands
-//   (dO^T, Q^T for dV/dK, K^T for dQ) come from ds_read_b64_tr_b16, so no
+// * streamed tiles are row-major [64 x DP] bf16 tiles in LDS whose 16-byte
+//   chunks are XOR-swizzled by row, conflict-free both for the 16-byte row
+//   reads of the S / dP products and for the ds_read_b64_tr_b16 reads that
+//   give the transposed operands (dO^T, Q^T for dV / dK, K^T for dQ), so no
 //   transposed copies are written;
-// * tiles read both ways (Q, dO in dK/dV; K in dQ) are XOR-swizzled by
-//   16-byte chunk, conflict-free for the 16-byte row reads of the S / dP
-//   products and for the transposed reads; row-read-only tiles are padded;
-// * the next tile is fetched into registers while the current one is
-//   consumed (double-buffered LDS, one barrier per tile);
-// * per-row LSE / delta are read as float4 for the four consecutive rows a
-//   lane's accumulator group covers.
+// * tiles move from HBM into an LDS ring by direct copies through buffer
+//   resources bounded at the last row, spread between the MFMAs;
+// * -lse * log2(e) and -delta enter the MFMA accumulators as their initial
+//   values (dK/dV) and the softmax scale is folded into the stationary K, so
+//   the element pass is exp2 and one multiply.
 #include "nxa_common.h"
 #include "nxa_launch.h"
 
