@@ -289,17 +289,23 @@ class _Prepared:
     def stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
 
-    def workspace(self, is_bwd: int) -> Optional[torch.Tensor]:
-        nbytes = _lib.lib().nxa_workspace_bytes(
+    def workspace_bytes(self, is_bwd: int) -> int:
+        return _lib.lib().nxa_workspace_bytes(
             ctypes.byref(self.desc), self.has_bias, self.has_mask, is_bwd
         )
+
+    def workspace(self, is_bwd: int) -> Optional[torch.Tensor]:
+        nbytes = self.workspace_bytes(is_bwd)
         if nbytes == 0:
             return None
         return torch.empty(nbytes, dtype=torch.uint8, device=self.device)
 
 
-def _forward(prep: _Prepared):
-    """Run ``nxa_fwd``; returns ``(o [nb,h,s,d], lse [nb,h,s], workspace)``."""
+def _forward(prep: _Prepared, for_bwd: bool = False):
+    """Run ``nxa_fwd``; returns ``(o [nb,h,s,d], lse [nb,h,s], workspace)``.
+
+    With ``for_bwd`` the workspace is sized for the backward as well (it
+    starts with the forward's tile map), so the backward reuses it as is."""
     lib = _lib.lib()
     o = torch.empty(
         (prep.nb, prep.h, prep.s, prep.d), dtype=prep.dtype, device=prep.device
@@ -307,7 +313,7 @@ def _forward(prep: _Prepared):
     lse = torch.empty(
         (prep.nb, prep.h, prep.s), dtype=torch.float32, device=prep.device
     )
-    ws = prep.workspace(0)
+    ws = prep.workspace(1 if for_bwd else 0)
     _lib.check(
         lib.nxa_fwd(
             ctypes.byref(prep.desc),
@@ -365,12 +371,17 @@ def _backward(prep: _Prepared, o, lse, fwd_ws, dout, want_dbias: bool):
             (ob, oh, lq, prep.t), dtype=prep.bias.dtype, device=prep.device
         )
         dbias_str = (ctypes.c_int64 * 3)(oh * lq * prep.t, lq * prep.t, prep.t)
-    ws = prep.workspace(1)
+    # The workspace begins with the forward's tile map; a forward workspace
+    # already sized for the backward is reused in place.
     ready = 0
-    if prep.mask is not None and fwd_ws is not None:
-        n_tm = fwd_ws.numel()
-        ws[:n_tm].copy_(fwd_ws)
-        ready = 1
+    if fwd_ws is not None and fwd_ws.numel() >= prep.workspace_bytes(1):
+        ws = fwd_ws
+        ready = 1 if prep.mask is not None else 0
+    else:
+        ws = prep.workspace(1)
+        if prep.mask is not None and fwd_ws is not None:
+            ws[: fwd_ws.numel()].copy_(fwd_ws)
+            ready = 1
     _lib.check(
         lib.nxa_bwd(
             ctypes.byref(prep.desc),
@@ -406,7 +417,7 @@ class _SdpaHip(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, bias, mask, scale, causal):
         prep = _Prepared(q, k, v, bias, mask, scale, causal)
-        o, lse, ws = _forward(prep)
+        o, lse, ws = _forward(prep, for_bwd=any(ctx.needs_input_grad[:4]))
         ctx.prep = prep
         ctx.shapes = (tuple(q.shape), tuple(k.shape), tuple(v.shape))
         ctx.save_for_backward(o, lse, ws if ws is not None else torch.empty(0))

@@ -617,9 +617,29 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
       df[c] = ok ? ld16(dop + d) : zero_frag<bf16>();
     }
   }
+  // Per-row values of the backward, computed here for this block's rows
+  // (the dK/dV kernel that runs next reads them from the workspace):
+  // delta = sum_d O dO over the row (each lane of the pair l, l ^ 32 holds
+  // half of it) and lse * log2(e), both negated.
   const int64_t rowid = ((int64_t)b * p.H + h) * p.Lq + qc;
-  const float neg_lse2 = p.nlse2[rowid];
-  const float ndlt = p.ndelta[rowid];
+  float dacc = 0.f;
+  {
+    const bf16* op = (const bf16*)p.o + b * p.o_str[0] + h * p.o_str[1] +
+                     (int64_t)qc * p.o_str[2];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = c * KC + g * EPC;
+      const Frag of = (qok && d < p.D) ? ld16(op + d) : zero_frag<bf16>();
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) dacc = __builtin_fmaf((float)of[e], (float)df[c][e], dacc);
+    }
+  }
+  const float ndlt = -(dacc + shfl_xor32(dacc));
+  const float neg_lse2 = -p.lse[rowid] * kLog2e;
+  if (qok && g == 0) {
+    p.ndelta[rowid] = ndlt;
+    p.nlse2[rowid] = neg_lse2;
+  }
   const int64_t brow = VALU_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] +
                                        (int64_t)qc * p.bias_str[2]
                                  : 0;

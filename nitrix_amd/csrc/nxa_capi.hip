@@ -371,8 +371,11 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
   p.ndelta = reinterpret_cast<float*>(wsb + ws.delta);
   p.nlse2 = reinterpret_cast<float*>(
       wsb + ws.delta + align256((size_t)d->B * d->H * d->Lq * sizeof(float)));
-  if ((rc = launch("delta", stream,
-                   [&] { nxa::launch_delta(p, d->io_dtype, stream); })))
+  // bf16: the dQ kernel computes -delta and -lse * log2(e) for its own rows
+  // and runs first; fp32 has a pass of its own.
+  const bool bf16_io = d->io_dtype == NXA_BF16;
+  if (!bf16_io && (rc = launch("delta", stream,
+                               [&] { nxa::launch_delta(p, d->io_dtype, stream); })))
     return rc;
   if (mask) {
     rc = setup_tilemap(p, d, wsb + ws.tilemap, !tilemap_ready, stream);
@@ -394,10 +397,14 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
     }
   }
   const int dp = d->D <= 64 ? 64 : 128;
+  if (bf16_io &&
+      (rc = launch("dq", stream, [&] { nxa::launch_dq(p, d->io_dtype, dp, stream); })))
+    return rc;
   if ((rc = launch("dkdv", stream,
                    [&] { nxa::launch_dkdv(p, d->io_dtype, dp, stream); })))
     return rc;
-  if ((rc = launch("dq", stream, [&] { nxa::launch_dq(p, d->io_dtype, dp, stream); })))
+  if (!bf16_io &&
+      (rc = launch("dq", stream, [&] { nxa::launch_dq(p, d->io_dtype, dp, stream); })))
     return rc;
   if (dbias && dg.reduce) {
     rc = launch("dbias_reduce", stream, [&] {

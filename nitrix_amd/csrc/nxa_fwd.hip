@@ -11,53 +11,67 @@
 namespace nxa {
 
 // ---------------------------------------------------------------------------
-// Tile map.  One block per 64x64 tile of the mask's own (un-broadcast)
-// extent; writes bit0 = some entry kept, bit1 = every in-range entry kept.
+// Tile map.  One wave per pair of horizontally adjacent 64x64 tiles of the
+// mask's own (un-broadcast) extent, so every row read is one whole 128-byte
+// line: lane l reads 16 bytes (column chunk l % 8) of rows l / 8 + 8 k.
+// Writes bit0 = some entry kept, bit1 = every in-range entry kept; wave
+// ballots do the reductions (no block barriers).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void tilemap_kernel(const Params p, int MB,
                                                       int MH, int MQ, int MK,
                                                       int vec16) {
-  int id = blockIdx.x;
-  const int mk = id % MK;
-  id /= MK;
-  const int mq = id % MQ;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int MK2 = (MK + 1) / 2;  // tile pairs per tile row
+  const int64_t pair = (int64_t)blockIdx.x * 4 + wave;
+  if (pair >= (int64_t)MB * MH * MQ * MK2) return;  // wave-uniform
+  int64_t id = pair;
+  const int mk2 = (int)(id % MK2);
+  id /= MK2;
+  const int mq = (int)(id % MQ);
   id /= MQ;
-  const int mh = id % MH;
-  const int mb = id / MH;
-  const int t = threadIdx.x;
-  const int r = t >> 2, seg = t & 3;
-  const int r0 = mq * kTile, c0 = mk * kTile;
+  const int mh = (int)(id % MH);
+  const int mb = (int)(id / MH);
+  const int r0 = mq * kTile, c0 = mk2 * 2 * kTile;
   const int nrows = min(kTile, p.tm_rows - r0);
-  const int ncols = min(kTile, p.Lk - c0);
-  int any = 0, all = 1;
-  if (r < nrows) {
-    const uint8_t* m = p.mask + mb * p.mask_str[0] + mh * p.mask_str[1] +
-                       (int64_t)(r0 + r) * p.mask_str[2] + c0 + 16 * seg;
-    const int nc = ncols - 16 * seg;
-    if (vec16 && nc >= 16) {
-      const u32x4 w = *reinterpret_cast<const u32x4*>(m);
+  const int sub = lane & 7, rr = lane >> 3;
+  const int nc = min(2 * kTile, p.Lk - c0) - 16 * sub;  // in-range bytes of the chunk
+  const uint8_t* m0 = p.mask + mb * p.mask_str[0] + mh * p.mask_str[1] +
+                      (int64_t)r0 * p.mask_str[2] + c0 + 16 * sub;
+  bool any = false, all = true;
+  if (nc > 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t x = w[i];
+    for (int k = 0; k < kTile / 8; ++k) {
+      const int r = 8 * k + rr;
+      if (r < nrows) {
+        const uint8_t* m = m0 + (int64_t)r * p.mask_str[2];
+        if (vec16 && nc >= 16) {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(m);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int on = ((x >> (8 * j)) & 0xffu) != 0;
-          any |= on;
-          all &= on;
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t x = w[i];
+            // x has a zero byte iff (x - 0x01010101) & ~x & 0x80808080 != 0.
+            any = any || x != 0;
+            all = all && ((x - 0x01010101u) & ~x & 0x80808080u) == 0;
+          }
+        } else {
+          for (int j = 0; j < 16 && j < nc; ++j) {
+            const bool on = m[j] != 0;
+            any = any || on;
+            all = all && on;
+          }
         }
       }
-    } else {
-      for (int j = 0; j < 16; ++j)
-        if (j < nc) {
-          const int on = m[j] != 0;
-          any |= on;
-          all &= on;
-        }
     }
   }
-  any = __syncthreads_or(any);
-  all = __syncthreads_and(all);
-  if (t == 0) p.tilemap_out[blockIdx.x] = (uint8_t)(any | (all << 1));
+  const uint64_t anyb = __ballot(any), offb = __ballot(!all);
+  constexpr uint64_t kLeft = 0x0f0f0f0f0f0f0f0full;  // lanes with sub < 4
+  if (lane == 0) {
+    const int64_t t = (((int64_t)mb * MH + mh) * MQ + mq) * MK + 2 * mk2;
+    p.tilemap_out[t] = (uint8_t)(((anyb & kLeft) != 0) | (((offb & kLeft) == 0) << 1));
+    if (2 * mk2 + 1 < MK)
+      p.tilemap_out[t + 1] =
+          (uint8_t)(((anyb & ~kLeft) != 0) | (((offb & ~kLeft) == 0) << 1));
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -328,7 +342,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const Params p) {
 // ---------------------------------------------------------------------------
 void launch_tilemap(const Params& p, int MB, int MH, int MQ, int MK, int vec16,
                     hipStream_t stream) {
-  const int n = MB * MH * MQ * MK;
+  const int64_t pairs = (int64_t)MB * MH * MQ * ((MK + 1) / 2);
+  const int n = (int)((pairs + 3) / 4);
   hipLaunchKernelGGL(tilemap_kernel, dim3(n), dim3(256), 0, stream, p, MB, MH,
                      MQ, MK, vec16);
 }
