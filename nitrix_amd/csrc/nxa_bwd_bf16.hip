@@ -640,6 +640,29 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
     p.ndelta[rowid] = ndlt;
     p.nlse2[rowid] = neg_lse2;
   }
+  // The scale folds into the stationary Q (S^T then comes out in log2
+  // units), and -lse2 / -delta enter S^T / dP^T through one more MFMA per
+  // 32-key block: a column of ones times the per-query value split into two
+  // bf16 terms (hi + lo, exact to 2^-16 relative).  The element pass is then
+  // exp2 and one multiply.  Rounding Q * scale * log2(e) to bf16 perturbs a
+  // logit by at most 2^-9 sum_d |q'_d k_d|.
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) qf[c][e] = (bf16)((float)qf[c][e] * p.scale_log2);
+  auto split_hi = [](float v) -> float { return (float)(bf16)v; };
+  auto split_lo = [](float v, float hi) -> float {
+    return __builtin_isfinite(v) ? (float)(bf16)(v - hi) : 0.f;
+  };
+  Frag ones = zero_frag<bf16>(), blse = zero_frag<bf16>(), bdlt = zero_frag<bf16>();
+  if (g == 0) {
+    ones[0] = ones[1] = (bf16)1.0f;
+    const float lh = split_hi(neg_lse2), dh = split_hi(ndlt);
+    blse[0] = (bf16)lh;
+    blse[1] = (bf16)split_lo(neg_lse2, lh);
+    bdlt[0] = (bf16)dh;
+    bdlt[1] = (bf16)split_lo(ndlt, dh);
+  }
   const int64_t brow = VALU_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] +
                                        (int64_t)qc * p.bias_str[2]
                                  : 0;
@@ -647,13 +670,16 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
                                          h * p.mask_str[1] +
                                          (int64_t)qc * p.mask_str[2]
                                    : nullptr;
-  // Row bias: B[0][q] = h (or l) for every query, reduction row 0 only.
+  // Row bias: B[0][q] = log2(e) split into bf16 h + l for every query,
+  // reduction row 0 only (S^T is in log2 units).
+  constexpr float kL2eHi = 1.4453125f;                   // bf16(log2(e))
+  constexpr float kL2eLo = 1.4426950408889634f - kL2eHi;  // rounded to bf16 below
   Frag bdh = zero_frag<bf16>(), bdl = zero_frag<bf16>();
   if constexpr (ROW_BIAS) {
-    bdh[0] = (bf16)(g == 0 ? p.bias_h : 0.f);
-    bdl[0] = (bf16)(g == 0 ? p.bias_l : 0.f);
+    bdh[0] = (bf16)(g == 0 ? kL2eHi : 0.f);
+    bdl[0] = (bf16)(g == 0 ? kL2eLo : 0.f);
   }
-  const bool bias_l = ROW_BIAS && p.bias_l != 0.f;  // uniform
+  constexpr bool bias_l = ROW_BIAS;
   // The stationary loads complete here, so the waits in the tile loop only
   // count tile copies.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -777,18 +803,17 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
       // dP chunk j / 2 (j odd); A fragments are read PD products ahead, and
       // this wave's copies of tile i + NST - 1 ride along (one per four
       // products).
-      f32x16 s, dp;
-      bool fresh = true;
+      f32x16 s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, blse, f32x16{}, 0, 0, 0);
+      f32x16 dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, bdlt, f32x16{}, 0, 0, 0);
       if constexpr (ROW_BIAS) {
         const uint32_t rb = at + 2 * TILE_BYTES + wave * 256;
         Frag a = zero_frag<bf16>();
         const bf16 bv = *(const lds_bf16*)(uintptr_t)(rb + 2 * (kb * 32 + c32));
         a[0] = g == 0 ? bv : (bf16)0.f;
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bdh, f32x16{}, 0, 0, 0);
+        M::run(s, a, bdh);
         if (bias_l) M::run(s, a, bdl);
-        fresh = false;
       }
-      constexpr int NP = 2 * NC, PD = (DP == 128 && ROW_BIAS) ? 4 : 8;
+      constexpr int NP = 2 * NC, PD = DP == 128 ? (ROW_BIAS ? 3 : 4) : 8;
       auto afrag = [&](int j) NXA_INLINE -> Frag {
         const uint32_t base = ka[j >> 1] + ((j & 1) ? TILE_BYTES : 0);
         return *(const lds_frag*)(uintptr_t)(base + kb * (32 * DP * 2));
@@ -799,17 +824,10 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
 #pragma unroll
       for (int j = 0; j < NP; ++j) {
         const int m = j >> 1;
-        if (j & 1) {
-          if (j == 1)
-            dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(abuf[j % PD], df[m], f32x16{}, 0, 0, 0);
-          else
-            M::run(dp, abuf[j % PD], df[m]);
-        } else {
-          if (fresh && j == 0)
-            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(abuf[j % PD], qf[m], f32x16{}, 0, 0, 0);
-          else
-            M::run(s, abuf[j % PD], qf[m]);
-        }
+        if (j & 1)
+          M::run(dp, abuf[j % PD], df[m]);
+        else
+          M::run(s, abuf[j % PD], qf[m]);
         if (j + PD < NP) abuf[j % PD] = afrag(j + PD);
         const int pc = kb * NP + j;  // product count in this tile
         if ((pc & 3) == 3 && (pc >> 2) < CPT) copy(sn, stn, pc >> 2);
@@ -841,7 +859,7 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int r = 4 * c + j;
-            float x = __builtin_fmaf(s[r], p.scale_log2, neg_lse2);
+            float x = s[r];
             if constexpr (GEN) {
               const int kk = key0 + j;
               if constexpr (VALU_BIAS) x = __builtin_fmaf(bv[j], kLog2e, x);
@@ -849,7 +867,7 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
               if (CAUSAL) keep = keep && kk <= qrow;
               x = keep ? x : -INFINITY;
             }
-            dp[r] = fast_exp2(x) * (dp[r] + ndlt);
+            dp[r] = fast_exp2(x) * dp[r];
           }
         }
 #pragma unroll
