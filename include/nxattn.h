@@ -51,7 +51,7 @@ extern "C" {
 
 #define NXA_VERSION 1
 
-typedef enum { NXA_BF16 = 0, NXA_F32 = 1 } nxa_dtype;
+typedef enum { NXA_BF16 = 0, NXA_F32 = 1, NXA_F16 = 2 } nxa_dtype;
 
 enum {
   NXA_OK = 0,
@@ -65,7 +65,7 @@ enum {
 };
 
 typedef struct {
-  int32_t B, H, Lq, Lk, D;  /* D <= 128, D % 8 == 0 (bf16) or % 4 (fp32)    */
+  int32_t B, H, Lq, Lk, D;  /* D <= 128, D % 8 == 0 (bf16, fp16) or % 4 (fp32) */
   int32_t io_dtype;         /* nxa_dtype of q, k, v, o, dO, dq, dk, dv       */
   int32_t bias_dtype;       /* nxa_dtype of bias and dbias                   */
   int32_t causal;           /* nonzero: keep key j for query i iff j <= i    */

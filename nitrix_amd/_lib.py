@@ -16,6 +16,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / 'libnxattn.so'
 
 NXA_BF16 = 0
 NXA_F32 = 1
+NXA_F16 = 2
 
 NXA_OK = 0
 NXA_E_ARG = -1

@@ -47,7 +47,13 @@ __all__ = [
 # RMS-norm epsilon for qk-norm (_reference.py:32).
 _QK_RMS_EPS = 1e-6
 
-_IO_DTYPES = {torch.bfloat16: _lib.NXA_BF16, torch.float32: _lib.NXA_F32}
+_IO_DTYPES = {
+    torch.bfloat16: _lib.NXA_BF16,
+    torch.float16: _lib.NXA_F16,
+    torch.float32: _lib.NXA_F32,
+}
+# Bias dtypes the kernels read natively (others are upcast to float32).
+_BIAS_DTYPES = _IO_DTYPES
 _MAX_HEAD_DIM = 128
 
 
@@ -153,13 +159,13 @@ def reference_scaled_dot_product_attention(
 def _check_tileable(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
     """Reject shapes the gfx950 kernels cannot run (``attention.py:708-765``).
 
-    Accepts bf16 or fp32 (q, k, v of one dtype), ``d_v == d``, head dim up to
-    128 (a multiple of 8 for bf16, of 4 for fp32) and any positive query / key
-    lengths (tails are predicated in the kernels).
+    Accepts bf16, fp16 or fp32 (q, k, v of one dtype), ``d_v == d``, head dim
+    up to 128 (a multiple of 8 for the 16-bit types, of 4 for fp32) and any
+    positive query / key lengths (tails are predicated in the kernels).
     """
     if q.dtype not in _IO_DTYPES:
         raise HipNotTileable(
-            f'fused attention supports bfloat16 and float32; got {q.dtype}.'
+            f'fused attention supports bfloat16, float16 and float32; got {q.dtype}.'
         )
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise HipNotTileable(
@@ -171,7 +177,7 @@ def _check_tileable(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         raise HipNotTileable(
             f'fused attention requires d_v == d; got d={d}, d_v={d_v}.'
         )
-    epc = 8 if q.dtype == torch.bfloat16 else 4
+    epc = 4 if q.dtype == torch.float32 else 8
     if d > _MAX_HEAD_DIM or d % epc != 0:
         raise HipNotTileable(
             f'fused attention requires head dim <= {_MAX_HEAD_DIM} and a '
@@ -238,7 +244,7 @@ class _Prepared:
         self.s, self.t, self.d = s, t, d
         self.dtype = q.dtype
         self.device = q.device
-        self.epc = 8 if q.dtype == torch.bfloat16 else 4
+        self.epc = 4 if q.dtype == torch.float32 else 8
         self.q = _as_bhld(q, lead, self.nb, self.epc)
         self.k = _as_bhld(k, lead, self.nb, self.epc)
         self.v = _as_bhld(v, lead, self.nb, self.epc)
@@ -247,7 +253,7 @@ class _Prepared:
         self.bias = None
         if bias is not None:
             b = bias.to(self.device)
-            if b.dtype not in (torch.bfloat16, torch.float32):
+            if b.dtype not in _BIAS_DTYPES:
                 b = b.to(torch.float32)
             self.bias = _as_bhst(b, lead, self.nb, s, t)
         self.mask = None
@@ -261,9 +267,7 @@ class _Prepared:
         desc.B, desc.H, desc.Lq, desc.Lk, desc.D = self.nb, self.h, s, t, d
         desc.io_dtype = _IO_DTYPES[q.dtype]
         desc.bias_dtype = (
-            _lib.NXA_BF16
-            if self.bias is not None and self.bias.dtype == torch.bfloat16
-            else _lib.NXA_F32
+            _BIAS_DTYPES[self.bias.dtype] if self.bias is not None else _lib.NXA_F32
         )
         desc.causal = 1 if causal else 0
         desc.scale = float(scale)

@@ -1,5 +1,5 @@
 // Backward pass: delta = rowsum(O * dO), the fp32 dK/dV and dQ kernels (the
-// bf16 ones live in nxa_bwd_bf16.hip), the dbias reduction and the launchers.
+// 16-bit ones live in nxa_bwd16.hip), the dbias reduction and the launchers.
 // Two deterministic kernels
 // (no atomics): dK/dV (+ dbias) with a grid over key tiles, and dQ with a
 // grid over query tiles.  Both recompute P from the forward's LSE.
@@ -17,7 +17,9 @@ namespace nxa {
 // ---------------------------------------------------------------------------
 // ndelta[b, h, q] = -sum_d O[q, d] * dO[q, d]  (fp32) and nlse2 = -lse * log2(e),
 // so the backward kernels stream both per-row values straight from memory
-// (negated: the bf16 kernels start their MFMA accumulators at them).
+// (negated: the 16-bit kernels start their MFMA accumulators at them).  Only
+// fp32 I/O runs this pass; with 16-bit I/O the dQ kernel computes both for its
+// own rows.
 // 16 lanes per row.
 // ---------------------------------------------------------------------------
 template <typename T>
@@ -99,10 +101,7 @@ __device__ __forceinline__ void load_tile(const T* src, int64_t rs, int r0,
 
 __device__ __forceinline__ void store_dbias(const Params& p, int64_t off,
                                             float x) {
-  if (p.dbias_f32 || p.bias_dtype == kF32)
-    reinterpret_cast<float*>(p.dbias)[off] = x;
-  else
-    reinterpret_cast<bf16*>(p.dbias)[off] = (bf16)x;
+  store_elem(p.dbias_f32 ? kF32 : p.bias_dtype, p.dbias, off, x);
 }
 
 // ---------------------------------------------------------------------------
@@ -227,9 +226,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
         float x = s[qb][r] * p.scale_log2;
         if (p.has_bias) {
           const int64_t off = bbase + (int64_t)qc * p.bias_str[2];
-          const float bv = p.bias_dtype == kBF16
-                               ? (float)reinterpret_cast<const bf16*>(p.bias)[off]
-                               : reinterpret_cast<const float*>(p.bias)[off];
+          const float bv = load_elem(p.bias_dtype, p.bias, off);
           x = __builtin_fmaf(bv, kLog2e, x);
         }
         bool keep = true;
@@ -450,10 +447,7 @@ __global__ __launch_bounds__(256) void dbias_reduce_kernel(
     for (int h = (OH == 1 ? 0 : oh); h < (OH == 1 ? p.H : oh + 1); ++h)
       acc += ws[(((int64_t)b * p.H + h) * LQ + q) * p.Lk + k];
   const int64_t off = ob * s0 + oh * s1 + q * s2 + k;
-  if (p.bias_dtype == kF32)
-    reinterpret_cast<float*>(out)[off] = acc;
-  else
-    reinterpret_cast<bf16*>(out)[off] = (bf16)acc;
+  store_elem(p.bias_dtype, out, off, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -462,10 +456,8 @@ __global__ __launch_bounds__(256) void dbias_reduce_kernel(
 void launch_delta(const Params& p, int io_dtype, hipStream_t stream) {
   const int rows = p.B * p.H * p.Lq;
   const int n = (rows + 15) / 16;
-  if (io_dtype == kBF16)
-    hipLaunchKernelGGL(delta_kernel<bf16>, dim3(n), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL(delta_kernel<float>, dim3(n), dim3(256), 0, stream, p);
+  (void)io_dtype;  // fp32 only (see delta_kernel)
+  hipLaunchKernelGGL(delta_kernel<float>, dim3(n), dim3(256), 0, stream, p);
 }
 
 template <typename T, int DP>
@@ -476,8 +468,8 @@ static void launch_dkdv_t(Params p, hipStream_t stream) {
 }
 
 void launch_dkdv(const Params& p, int io_dtype, int dp, hipStream_t stream) {
-  if (io_dtype == kBF16) {
-    launch_dkdv_bf16(p, dp, stream);
+  if (io_dtype == kBF16 || io_dtype == kF16) {
+    launch_dkdv16(p, io_dtype, dp, stream);
   } else {
     if (dp == 64) launch_dkdv_t<float, 64>(p, stream);
     else launch_dkdv_t<float, 128>(p, stream);
@@ -492,8 +484,8 @@ static void launch_dq_t(Params p, hipStream_t stream) {
 }
 
 void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream) {
-  if (io_dtype == kBF16) {
-    launch_dq_bf16(p, dp, stream);
+  if (io_dtype == kBF16 || io_dtype == kF16) {
+    launch_dq16(p, io_dtype, dp, stream);
   } else {
     if (dp == 64) launch_dq_t<float, 64>(p, stream);
     else launch_dq_t<float, 128>(p, stream);

@@ -1,4 +1,5 @@
-// bf16 backward kernels for gfx950: dK/dV (+ dbias) and dQ.
+// 16-bit (bf16 / fp16 I/O) backward kernels for gfx950: dK/dV (+ dbias) and
+// dQ, templated on the element type T (the MFMA and conversions follow it).
 //
 // Same math as the reference's two backward Pallas kernels
 // (src/nitrix/_kernels/cuda/attention.py:272-332 dK/dV, :335-387 dQ):
@@ -8,16 +9,17 @@
 // and streams key tiles.
 //
 // Layout choices for CDNA4:
-// * streamed tiles are row-major [64 x DP] bf16 tiles in LDS whose 16-byte
+// * streamed tiles are row-major [64 x DP] 16-bit tiles in LDS whose 16-byte
 //   chunks are XOR-swizzled by row, conflict-free both for the 16-byte row
 //   reads of the S / dP products and for the ds_read_b64_tr_b16 reads that
 //   give the transposed operands (dO^T, Q^T for dV / dK, K^T for dQ), so no
 //   transposed copies are written;
 // * tiles move from HBM into an LDS ring by direct copies through buffer
 //   resources bounded at the last row, spread between the MFMAs;
-// * -lse * log2(e) and -delta enter the MFMA accumulators as their initial
-//   values (dK/dV) and the softmax scale is folded into the stationary K, so
-//   the element pass is exp2 and one multiply.
+// * -delta enters the dP accumulators as their initial value; the logits
+//   come out of one FMA per element, S * scale * log2(e) - lse * log2(e), on
+//   the exact fp32 products (scaling Q or K before the 16-bit rounding would
+//   perturb every logit by 2^-9 of its size in bf16).
 #include "nxa_common.h"
 #include "nxa_launch.h"
 
@@ -34,25 +36,20 @@ constexpr int kMaxBwdTiles = 1024;
 enum : int { kDbNone = 0, kDbFull = 1, kDbColsum = 2 };
 
 __device__ __forceinline__ void store_db(const Params& p, int64_t off, float x) {
-  if (p.dbias_f32 || p.bias_dtype == kF32)
-    reinterpret_cast<float*>(p.dbias)[off] = x;
-  else
-    reinterpret_cast<bf16*>(p.dbias)[off] = (bf16)x;
+  store_elem(p.dbias_f32 ? kF32 : p.bias_dtype, p.dbias, off, x);
 }
 
 __device__ __forceinline__ float load_bias1(const Params& p, int64_t off) {
-  return p.bias_dtype == kBF16 ? (float)reinterpret_cast<const bf16*>(p.bias)[off]
-                               : reinterpret_cast<const float*>(p.bias)[off];
+  return load_elem(p.bias_dtype, p.bias, off);
 }
 
 // ---------------------------------------------------------------------------
 // dK / dV.  Block = 8 waves over 128 keys.  Waves w and w + 4 own the same
 // 32 keys (the key is the lane's column, so P and dS feed the dV / dK
 // products from registers) and share SIMD w:
-//   * the P wave (w < 4) holds K' = K * scale * log2(e) stationary and starts
-//     its accumulator at -lse2, so S' = Q K'^T - lse2 and P = exp2(S')
-//     directly; it publishes P (fp32, in register order) through LDS and
-//     accumulates dV^T += dO^T P;
+//   * the P wave (w < 4) holds K stationary, forms P = exp2(S c - lse2)
+//     (c = scale * log2(e), one FMA per element on the fp32 scores), publishes
+//     P (as T, in register order) through LDS and accumulates dV^T += dO^T P;
 //   * the dS wave (w >= 4) holds V stationary and starts at -delta, so its
 //     product is dP - delta; dS = P (dP - delta) with P read back from LDS,
 //     dK^T += Q^T dS (and dbias).
@@ -64,14 +61,11 @@ __device__ __forceinline__ float load_bias1(const Params& p, int64_t off) {
 // HBM into a 3-stage LDS ring by direct copies two tiles ahead; each wave
 // waits only for its own copies of the next tile before the tile barrier.
 //
-// Rounding K * scale * log2(e) to bf16 perturbs each logit by at most
-// 2^-9 sum_d |q_d k'_d| (about 1e-3 in log2 units for unit-variance inputs
-// at D = 128), well inside the bf16 output budget.
 // ---------------------------------------------------------------------------
-template <int DP, bool HAS_BIAS, bool CAUSAL, int DBM>
-__global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
-  using M = Mma<bf16>;
-  using Frag = bf16x8;
+template <typename T, int DP, bool HAS_BIAS, bool CAUSAL, int DBM>
+__global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
+  using M = Mma<T>;
+  using Frag = typename M::Frag;
   constexpr int EPC = 8, KC = 16;
   constexpr int BNK = 128, BQ = 64, NW = 8, NST = 3;
   constexpr int NC = DP / KC, NDB = DP / 32, FPB = M::FRAGS_PER_BLOCK;
@@ -100,8 +94,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
   const bool kok = key < p.Lk;
   const int kc = kok ? key : p.Lk - 1;
 
-  const bf16* qp = (const bf16*)p.q + b * p.q_str[0] + h * p.q_str[1];
-  const bf16* dop = (const bf16*)p.dout + b * p.o_str[0] + h * p.o_str[1];
+  const T* qp = (const T*)p.q + b * p.q_str[0] + h * p.q_str[1];
+  const T* dop = (const T*)p.dout + b * p.o_str[0] + h * p.o_str[1];
   const float* nlp = p.nlse2 + ((int64_t)b * p.H + h) * p.Lq;
   const float* ndp = p.ndelta + ((int64_t)b * p.H + h) * p.Lq;
   const int64_t qs = p.q_str[2], os = p.o_str[2];
@@ -156,22 +150,17 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
     return t;
   };
 
-  // Stationary B operands for this lane's key: K' (P wave) or V (dS wave).
+  // Stationary B operands for this lane's key: K (P wave) or V (dS wave).
   Frag bfr[NC];
   {
-    const bf16* src = pw ? (const bf16*)p.k + b * p.k_str[0] + h * p.k_str[1] +
-                               (int64_t)kc * p.k_str[2]
-                         : (const bf16*)p.v + b * p.v_str[0] + h * p.v_str[1] +
-                               (int64_t)kc * p.v_str[2];
+    const T* src = pw ? (const T*)p.k + b * p.k_str[0] + h * p.k_str[1] +
+                            (int64_t)kc * p.k_str[2]
+                      : (const T*)p.v + b * p.v_str[0] + h * p.v_str[1] +
+                            (int64_t)kc * p.v_str[2];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int d = c * KC + g * EPC;
-      Frag f = (kok && d < p.D) ? ld16(src + d) : zero_frag<bf16>();
-      if (pw) {
-#pragma unroll
-        for (int e = 0; e < EPC; ++e) f[e] = (bf16)((float)f[e] * p.scale_log2);
-      }
-      bfr[c] = f;
+      bfr[c] = (kok && d < p.D) ? ld16(src + d) : zero_frag<T>();
     }
   }
   f32x16 acc[NDB];  // dV^T (P wave) or dK^T (dS wave)
@@ -268,7 +257,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
     }
   // Per-row values: rows 8c + 4g .. +3 of each 32-row block.
   const uint32_t rvoff = ROWS_OFF + (pw ? 0 : BQ * 4) + 16 * g;
-  // P exchange: the lane's two bf16 fragments per query block, 1 KB apart.
+  // P exchange: the lane's two T fragments per query block, 1 KB apart.
   const uint32_t poff = pbuf + (wave & 3) * (2 * 2 * 1024) + 16 * lane;
 
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -287,10 +276,13 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
     return r;
   };
 
-  // Row products of one tile: x[qb] = A B^T + (per-row value), A = Q (P
-  // wave) or dO (dS wave) of the tile in stage `at`, two 32-query blocks.
+  // Row products of one tile, two 32-query blocks: A B^T with A = Q (P
+  // wave) or dO (dS wave) of the tile in stage `at`.  The dS wave's
+  // accumulators start at the per-row values (x = dP - delta); the P wave's
+  // start at zero and its per-row values (-lse2) land in `rows`.
   // `between(j)` runs after product j (the dS wave's tile copies).
-  auto row_products = [&](uint32_t at, f32x16 (&x)[2], auto&& between) NXA_INLINE {
+  auto row_products = [&](uint32_t at, f32x16 (&x)[2], f32x16 (&rows)[2],
+                          auto&& between) NXA_INLINE {
     const uint32_t rt = at + (pw ? 0 : TILE_BYTES);
     uint32_t ra[NC];
 #pragma unroll
@@ -302,7 +294,14 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
       for (int c = 0; c < 4; ++c) {
         const f32x4 v4 = *(const lds_f32x4*)(uintptr_t)(rv + (qb * 32 + 8 * c) * 4);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) x[qb][4 * c + j] = v4[j];
+        for (int j = 0; j < 4; ++j) {
+          if (pw) {
+            rows[qb][4 * c + j] = v4[j];
+            x[qb][4 * c + j] = 0.f;
+          } else {
+            x[qb][4 * c + j] = v4[j];
+          }
+        }
       }
     // Product j: query block j & 1, head-dim chunk pair j >> 1.  The A
     // fragments are read PD products ahead (a rotating register buffer) so
@@ -350,14 +349,14 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
       }
   };
 
-  // P wave, tile t in stage st: P = exp2(S'), published (bf16) in P buffer
+  // P wave, tile t in stage st: P = exp2(S'), published (as T) in P buffer
   // `par`, then dV^T += dO^T P.
   auto p_tile = [&](int t, int st, int par) NXA_INLINE {
     const uint32_t at = lds0 + st * STAGE_BYTES;
     const int q0 = t * BQ;
     __builtin_amdgcn_s_setprio(DKDV_PRIO);  // the exp pass depends on these
-    f32x16 x[2];
-    row_products(at, x, [](int) {});
+    f32x16 x[2], rows[2];
+    row_products(at, x, rows, [](int) {});
     __builtin_amdgcn_s_setprio(0);
     const int cls = ucls >= 0 ? ucls : tclass(t);
     const bool need_mask = mask_rows && !(cls & 2);
@@ -373,7 +372,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
       constexpr bool ADD = decltype(add_tag)::value;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float xv = x[qb][r];
+        float xv = __builtin_fmaf(x[qb][r], p.scale_log2, rows[qb][r]);
         if constexpr (ADD) xv += kadd;
         if constexpr (GEN) {
           const int q = q0 + qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -414,8 +413,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
   auto ds_tile = [&](int t, int st, int par, const TileSrc& s, int stn) NXA_INLINE {
     const uint32_t at = lds0 + st * STAGE_BYTES;
     const int q0 = t * BQ;
-    f32x16 x[2];
-    row_products(at, x, [&](int j) NXA_INLINE {
+    f32x16 x[2], rows[2];
+    row_products(at, x, rows, [&](int j) NXA_INLINE {
       if (j & 1) copy(s, stn, j >> 1);
     });
     __builtin_amdgcn_s_setprio(DKDV_PRIO);  // dS and dK form the longer chain
@@ -494,7 +493,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
 
   if (kok) {
     if (!pw) {
-      bf16* dkp = (bf16*)p.dk + b * p.k_str[0] + h * p.k_str[1] + (int64_t)key * p.k_str[2];
+      T* dkp = (T*)p.dk + b * p.k_str[0] + h * p.k_str[1] + (int64_t)key * p.k_str[2];
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -503,7 +502,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
           if (d0 < p.D) store4(dkp + d0, acc[db], 4 * c, p.scale);
         }
     } else {
-      bf16* dvp = (bf16*)p.dv + b * p.v_str[0] + h * p.v_str[1] + (int64_t)key * p.v_str[2];
+      T* dvp = (T*)p.dv + b * p.v_str[0] + h * p.v_str[1] + (int64_t)key * p.v_str[2];
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -531,10 +530,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_bf16_kernel(const Params p) {
 // broadcasts over queries (BMODE kFbRow) enters S^T through one more MFMA
 // per 32-key block, as in the forward; other biases take the element pass.
 // ---------------------------------------------------------------------------
-template <int DP, int BMODE, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
-  using M = Mma<bf16>;
-  using Frag = bf16x8;
+template <typename T, int DP, int BMODE, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void dq16_kernel(const Params p) {
+  using M = Mma<T>;
+  using Frag = typename M::Frag;
+  using MB = Mma<bf16>;  // the ones-column product of -delta
   constexpr int EPC = 8, KC = 16;
   constexpr int NW = 4, BM = NW * 32, BN = 64;
   constexpr int NC = DP / KC, NDB = DP / 32, FPB = M::FRAGS_PER_BLOCK;
@@ -564,8 +564,8 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
   const bool qok = qrow < p.Lq;
   const int qc = qok ? qrow : p.Lq - 1;
 
-  const bf16* kp = (const bf16*)p.k + b * p.k_str[0] + h * p.k_str[1];
-  const bf16* vp = (const bf16*)p.v + b * p.v_str[0] + h * p.v_str[1];
+  const T* kp = (const T*)p.k + b * p.k_str[0] + h * p.k_str[1];
+  const T* vp = (const T*)p.v + b * p.v_str[0] + h * p.v_str[1];
   const int64_t ks = p.k_str[2], vs = p.v_str[2];
 
   // --- active key tiles of this block (tile-map classes) --------------------
@@ -605,16 +605,16 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
   // --- stationary Q^T, dO^T fragments and per-row values ------------------------
   Frag qf[NC], df[NC];
   {
-    const bf16* qp = (const bf16*)p.q + b * p.q_str[0] + h * p.q_str[1] +
-                     (int64_t)qc * p.q_str[2];
-    const bf16* dop = (const bf16*)p.dout + b * p.o_str[0] + h * p.o_str[1] +
-                      (int64_t)qc * p.o_str[2];
+    const T* qp = (const T*)p.q + b * p.q_str[0] + h * p.q_str[1] +
+                  (int64_t)qc * p.q_str[2];
+    const T* dop = (const T*)p.dout + b * p.o_str[0] + h * p.o_str[1] +
+                   (int64_t)qc * p.o_str[2];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int d = c * KC + g * EPC;
       const bool ok = qok && d < p.D;
-      qf[c] = ok ? ld16(qp + d) : zero_frag<bf16>();
-      df[c] = ok ? ld16(dop + d) : zero_frag<bf16>();
+      qf[c] = ok ? ld16(qp + d) : zero_frag<T>();
+      df[c] = ok ? ld16(dop + d) : zero_frag<T>();
     }
   }
   // Per-row values of the backward, computed here for this block's rows
@@ -624,12 +624,12 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
   const int64_t rowid = ((int64_t)b * p.H + h) * p.Lq + qc;
   float dacc = 0.f;
   {
-    const bf16* op = (const bf16*)p.o + b * p.o_str[0] + h * p.o_str[1] +
-                     (int64_t)qc * p.o_str[2];
+    const T* op = (const T*)p.o + b * p.o_str[0] + h * p.o_str[1] +
+                  (int64_t)qc * p.o_str[2];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int d = c * KC + g * EPC;
-      const Frag of = (qok && d < p.D) ? ld16(op + d) : zero_frag<bf16>();
+      const Frag of = (qok && d < p.D) ? ld16(op + d) : zero_frag<T>();
 #pragma unroll
       for (int e = 0; e < EPC; ++e) dacc = __builtin_fmaf((float)of[e], (float)df[c][e], dacc);
     }
@@ -640,26 +640,19 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
     p.ndelta[rowid] = ndlt;
     p.nlse2[rowid] = neg_lse2;
   }
-  // The scale folds into the stationary Q (S^T then comes out in log2
-  // units), and -lse2 / -delta enter S^T / dP^T through one more MFMA per
-  // 32-key block: a column of ones times the per-query value split into two
-  // bf16 terms (hi + lo, exact to 2^-16 relative).  The element pass is then
-  // exp2 and one multiply.  Rounding Q * scale * log2(e) to bf16 perturbs a
-  // logit by at most 2^-9 sum_d |q'_d k_d|.
-#pragma unroll
-  for (int c = 0; c < NC; ++c)
-#pragma unroll
-    for (int e = 0; e < EPC; ++e) qf[c][e] = (bf16)((float)qf[c][e] * p.scale_log2);
+  // -delta enters dP^T through one more MFMA per 32-key block: a column of
+  // ones times the per-query value split into two bf16 terms (hi + lo, exact
+  // to 2^-16 relative; bf16 for either T, whose range covers any finite fp32
+  // value).  The logits are one FMA per element on the exact fp32 scores,
+  // S c - lse2 (c = scale * log2(e)), and dS^T = exp2(.) (dP - delta).
   auto split_hi = [](float v) -> float { return (float)(bf16)v; };
   auto split_lo = [](float v, float hi) -> float {
     return __builtin_isfinite(v) ? (float)(bf16)(v - hi) : 0.f;
   };
-  Frag ones = zero_frag<bf16>(), blse = zero_frag<bf16>(), bdlt = zero_frag<bf16>();
+  typename MB::Frag ones = zero_frag<bf16>(), bdlt = zero_frag<bf16>();
   if (g == 0) {
     ones[0] = ones[1] = (bf16)1.0f;
-    const float lh = split_hi(neg_lse2), dh = split_hi(ndlt);
-    blse[0] = (bf16)lh;
-    blse[1] = (bf16)split_lo(neg_lse2, lh);
+    const float dh = split_hi(ndlt);
     bdlt[0] = (bf16)dh;
     bdlt[1] = (bf16)split_lo(ndlt, dh);
   }
@@ -670,14 +663,13 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
                                          h * p.mask_str[1] +
                                          (int64_t)qc * p.mask_str[2]
                                    : nullptr;
-  // Row bias: B[0][q] = log2(e) split into bf16 h + l for every query,
-  // reduction row 0 only (S^T is in log2 units).
-  constexpr float kL2eHi = 1.4453125f;                   // bf16(log2(e))
-  constexpr float kL2eLo = 1.4426950408889634f - kL2eHi;  // rounded to bf16 below
-  Frag bdh = zero_frag<bf16>(), bdl = zero_frag<bf16>();
+  // Row bias (of dtype T, as in the forward's row mode): B[0][q] = 1/scale
+  // split into the T terms h + l for every query, reduction row 0 only, so
+  // S^T accumulates bias / scale + K Q^T.
+  Frag bdh = zero_frag<T>(), bdl = zero_frag<T>();
   if constexpr (ROW_BIAS) {
-    bdh[0] = (bf16)(g == 0 ? kL2eHi : 0.f);
-    bdl[0] = (bf16)(g == 0 ? kL2eLo : 0.f);
+    bdh[0] = (T)(g == 0 ? p.bias_h : 0.f);
+    bdl[0] = (T)(g == 0 ? p.bias_l : 0.f);
   }
   constexpr bool bias_l = ROW_BIAS;
   // The stationary loads complete here, so the waits in the tile loop only
@@ -695,8 +687,8 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
   ksm.init(ks, p.D, wave, lane);
   vsm.init(vs, p.D, wave, lane);
   const uint32_t lds0 = lds_offset(smem);
-  const bf16* bp = ROW_BIAS ? (const bf16*)p.bias + b * p.bias_str[0] + h * p.bias_str[1]
-                            : nullptr;
+  const T* bp = ROW_BIAS ? (const T*)p.bias + b * p.bias_str[0] + h * p.bias_str[1]
+                         : nullptr;
   struct TileSrc {
     i32x4 k, v, r;  // K rows, V rows, bias row
   };
@@ -742,7 +734,7 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
     }
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
   typedef __attribute__((address_space(3))) Frag lds_frag;
-  typedef __attribute__((address_space(3))) bf16 lds_bf16;
+  typedef __attribute__((address_space(3))) T lds_t;
   typedef short i16x8 __attribute__((ext_vector_type(8)));
   auto tr_frag = [&](uint32_t a0, uint32_t a1) NXA_INLINE -> Frag {
     const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a0);
@@ -803,14 +795,14 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
       // dP chunk j / 2 (j odd); A fragments are read PD products ahead, and
       // this wave's copies of tile i + NST - 1 ride along (one per four
       // products).
-      f32x16 s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, blse, f32x16{}, 0, 0, 0);
-      f32x16 dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, bdlt, f32x16{}, 0, 0, 0);
+      f32x16 s;
+      f32x16 dp = MB::first(ones, bdlt);
       if constexpr (ROW_BIAS) {
         const uint32_t rb = at + 2 * TILE_BYTES + wave * 256;
-        Frag a = zero_frag<bf16>();
-        const bf16 bv = *(const lds_bf16*)(uintptr_t)(rb + 2 * (kb * 32 + c32));
-        a[0] = g == 0 ? bv : (bf16)0.f;
-        M::run(s, a, bdh);
+        Frag a = zero_frag<T>();
+        const T bv = *(const lds_t*)(uintptr_t)(rb + 2 * (kb * 32 + c32));
+        a[0] = g == 0 ? bv : (T)0.f;
+        s = M::first(a, bdh);
         if (bias_l) M::run(s, a, bdl);
       }
       constexpr int NP = 2 * NC, PD = DP == 128 ? (ROW_BIAS ? 3 : 4) : 8;
@@ -826,6 +818,8 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
         const int m = j >> 1;
         if (j & 1)
           M::run(dp, abuf[j % PD], df[m]);
+        else if (!ROW_BIAS && j == 0)
+          s = M::first(abuf[0], qf[0]);
         else
           M::run(s, abuf[j % PD], qf[m]);
         if (j + PD < NP) abuf[j % PD] = afrag(j + PD);
@@ -859,7 +853,7 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int r = 4 * c + j;
-            float x = s[r];
+            float x = __builtin_fmaf(s[r], p.scale_log2, neg_lse2);
             if constexpr (GEN) {
               const int kk = key0 + j;
               if constexpr (VALU_BIAS) x = __builtin_fmaf(bv[j], kLog2e, x);
@@ -904,7 +898,7 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   if (qok) {
-    bf16* dqp = (bf16*)p.dq + b * p.q_str[0] + h * p.q_str[1] + (int64_t)qrow * p.q_str[2];
+    T* dqp = (T*)p.dq + b * p.q_str[0] + h * p.q_str[1] + (int64_t)qrow * p.q_str[2];
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -918,62 +912,74 @@ __global__ __launch_bounds__(256, 2) void dq_bf16_kernel(const Params p) {
 // ---------------------------------------------------------------------------
 // Launchers.
 // ---------------------------------------------------------------------------
-template <int DP, bool HB, bool CA, int DBM>
-static void launch_dkdv_bf16_t(Params p, hipStream_t stream) {
+template <typename T, int DP, bool HB, bool CA, int DBM>
+static void launch_dkdv16_t(Params p, hipStream_t stream) {
   p.nkt = (p.Lk + 127) / 128;
   const int n = p.B * p.H * p.nkt;
-  hipLaunchKernelGGL((dkdv_bf16_kernel<DP, HB, CA, DBM>), dim3(n), dim3(512), 0,
+  hipLaunchKernelGGL((dkdv16_kernel<T, DP, HB, CA, DBM>), dim3(n), dim3(512), 0,
                      stream, p);
 }
 
-template <int DP, bool CA>
-static void launch_dkdv_bf16_db(const Params& p, hipStream_t stream) {
+template <typename T, int DP, bool CA>
+static void launch_dkdv16_db(const Params& p, hipStream_t stream) {
   if (!p.has_bias) {
-    launch_dkdv_bf16_t<DP, false, CA, kDbNone>(p, stream);
+    launch_dkdv16_t<T, DP, false, CA, kDbNone>(p, stream);
   } else if (p.dbias_mode == kDbiasFull) {
-    launch_dkdv_bf16_t<DP, true, CA, kDbFull>(p, stream);
+    launch_dkdv16_t<T, DP, true, CA, kDbFull>(p, stream);
   } else if (p.dbias_mode == kDbiasColsum) {
-    launch_dkdv_bf16_t<DP, true, CA, kDbColsum>(p, stream);
+    launch_dkdv16_t<T, DP, true, CA, kDbColsum>(p, stream);
   } else {
-    launch_dkdv_bf16_t<DP, true, CA, kDbNone>(p, stream);
+    launch_dkdv16_t<T, DP, true, CA, kDbNone>(p, stream);
   }
 }
 
-void launch_dkdv_bf16(const Params& p, int dp, hipStream_t stream) {
+template <typename T>
+static void launch_dkdv16_dp(const Params& p, int dp, hipStream_t stream) {
   if (dp == 64) {
-    if (p.causal) launch_dkdv_bf16_db<64, true>(p, stream);
-    else launch_dkdv_bf16_db<64, false>(p, stream);
+    if (p.causal) launch_dkdv16_db<T, 64, true>(p, stream);
+    else launch_dkdv16_db<T, 64, false>(p, stream);
   } else {
-    if (p.causal) launch_dkdv_bf16_db<128, true>(p, stream);
-    else launch_dkdv_bf16_db<128, false>(p, stream);
+    if (p.causal) launch_dkdv16_db<T, 128, true>(p, stream);
+    else launch_dkdv16_db<T, 128, false>(p, stream);
   }
 }
 
-template <int DP, int BMODE, bool CA>
-static void launch_dq_bf16_t(Params p, hipStream_t stream) {
+void launch_dkdv16(const Params& p, int io_dtype, int dp, hipStream_t stream) {
+  if (io_dtype == kF16) launch_dkdv16_dp<f16>(p, dp, stream);
+  else launch_dkdv16_dp<bf16>(p, dp, stream);
+}
+
+template <typename T, int DP, int BMODE, bool CA>
+static void launch_dq16_t(Params p, hipStream_t stream) {
   p.nqt = (p.Lq + 127) / 128;
   const int n = p.B * p.H * p.nqt;
-  hipLaunchKernelGGL((dq_bf16_kernel<DP, BMODE, CA>), dim3(n), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((dq16_kernel<T, DP, BMODE, CA>), dim3(n), dim3(256), 0, stream, p);
 }
 
-template <int DP, int BMODE>
-static void launch_dq_bf16_c(const Params& p, hipStream_t stream) {
-  if (p.causal) launch_dq_bf16_t<DP, BMODE, true>(p, stream);
-  else launch_dq_bf16_t<DP, BMODE, false>(p, stream);
+template <typename T, int DP, int BMODE>
+static void launch_dq16_c(const Params& p, hipStream_t stream) {
+  if (p.causal) launch_dq16_t<T, DP, BMODE, true>(p, stream);
+  else launch_dq16_t<T, DP, BMODE, false>(p, stream);
 }
 
 // Bias: through an MFMA when it broadcasts over queries (the forward's row
 // mode), else the element pass.
-template <int DP>
-static void launch_dq_bf16_flags(const Params& p, hipStream_t stream) {
-  if (!p.has_bias) launch_dq_bf16_c<DP, kFbNone>(p, stream);
-  else if (p.fwd_bias == kFbRow) launch_dq_bf16_c<DP, kFbRow>(p, stream);
-  else launch_dq_bf16_c<DP, kFbValu>(p, stream);
+template <typename T, int DP>
+static void launch_dq16_flags(const Params& p, hipStream_t stream) {
+  if (!p.has_bias) launch_dq16_c<T, DP, kFbNone>(p, stream);
+  else if (p.fwd_bias == kFbRow) launch_dq16_c<T, DP, kFbRow>(p, stream);
+  else launch_dq16_c<T, DP, kFbValu>(p, stream);
 }
 
-void launch_dq_bf16(const Params& p, int dp, hipStream_t stream) {
-  if (dp == 64) launch_dq_bf16_flags<64>(p, stream);
-  else launch_dq_bf16_flags<128>(p, stream);
+template <typename T>
+static void launch_dq16_dp(const Params& p, int dp, hipStream_t stream) {
+  if (dp == 64) launch_dq16_flags<T, 64>(p, stream);
+  else launch_dq16_flags<T, 128>(p, stream);
+}
+
+void launch_dq16(const Params& p, int io_dtype, int dp, hipStream_t stream) {
+  if (io_dtype == kF16) launch_dq16_dp<f16>(p, dp, stream);
+  else launch_dq16_dp<bf16>(p, dp, stream);
 }
 
 }  // namespace nxa

@@ -30,7 +30,9 @@ int fail(int code, const char* fmt, ...) {
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-int esize(int dt) { return dt == NXA_BF16 ? 2 : 4; }
+int esize(int dt) { return dt == NXA_F32 ? 4 : 2; }
+
+bool known_dtype(int dt) { return dt == NXA_BF16 || dt == NXA_F32 || dt == NXA_F16; }
 
 // ---------------------------------------------------------------------------
 // Profiling: HIP events around each launch while enabled.
@@ -74,11 +76,11 @@ int launch(const char* name, hipStream_t stream, F&& f) {
 // ---------------------------------------------------------------------------
 int check_desc(const nxa_desc* d, int has_bias, int has_mask) {
   if (!d) return fail(NXA_E_ARG, "descriptor is NULL");
-  if (d->io_dtype != NXA_BF16 && d->io_dtype != NXA_F32)
-    return fail(NXA_E_DTYPE, "io_dtype %d is not NXA_BF16 or NXA_F32",
+  if (!known_dtype(d->io_dtype))
+    return fail(NXA_E_DTYPE, "io_dtype %d is not NXA_BF16, NXA_F16 or NXA_F32",
                 d->io_dtype);
-  if (has_bias && d->bias_dtype != NXA_BF16 && d->bias_dtype != NXA_F32)
-    return fail(NXA_E_DTYPE, "bias_dtype %d is not NXA_BF16 or NXA_F32",
+  if (has_bias && !known_dtype(d->bias_dtype))
+    return fail(NXA_E_DTYPE, "bias_dtype %d is not NXA_BF16, NXA_F16 or NXA_F32",
                 d->bias_dtype);
   if (d->B <= 0 || d->H <= 0 || d->Lq <= 0 || d->Lk <= 0 || d->D <= 0)
     return fail(NXA_E_SHAPE, "extents must be positive (B=%d H=%d Lq=%d Lk=%d D=%d)",
@@ -190,19 +192,41 @@ float round_bf16(float x) {
   return r;
 }
 
-// Chooses how the bf16 forward adds the bias (nxa::FwdBias).  The MFMA modes
-// need a bf16 bias whose rows are 16-byte aligned whole 8-key chunks, and a
-// positive scale whose reciprocal splits into two normal bf16 terms h + l.
+// Round to the nearest fp16 (ties to even), returned as a float: 10 fraction
+// bits in the normal range, multiples of 2^-24 below 2^-14 (subnormals), inf
+// from 65520 up.
+float round_f16(float x) {
+  if (!std::isfinite(x)) return x;
+  if (std::fabs(x) >= 65520.f) return std::copysign(INFINITY, x);
+  if (std::fabs(x) < 6.103515625e-05f)
+    return std::nearbyint(x * 16777216.f) / 16777216.f;
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  u += 0xfffu + ((u >> 13) & 1u);
+  u &= 0xffffe000u;
+  float r;
+  std::memcpy(&r, &u, 4);
+  return r;
+}
+
+// Chooses how the 16-bit forward adds the bias (nxa::FwdBias).  The MFMA
+// modes need a bias of the I/O dtype whose rows are 16-byte aligned whole
+// 8-key chunks, and a positive scale whose reciprocal splits into two normal
+// terms h + l of that dtype.
 int fwd_bias_mode(const nxa_desc* d, const void* bias, float* h, float* l) {
   *h = *l = 0.f;
-  if (d->io_dtype != NXA_BF16 || d->bias_dtype != NXA_BF16) return nxa::kFbValu;
+  if (d->io_dtype == NXA_F32 || d->bias_dtype != d->io_dtype) return nxa::kFbValu;
   if (!(d->scale > 0.f) || !std::isfinite(d->scale)) return nxa::kFbValu;
+  const bool f16 = d->io_dtype == NXA_F16;
+  // Smallest normal and largest finite value of the dtype.
+  const float tiny = f16 ? 6.103515625e-05f : 1e-30f;
+  const float huge = f16 ? 65504.f : 1e30f;
   const float inv = 1.0f / d->scale;
-  const float hi = round_bf16(inv);
-  const float lo = round_bf16(inv - hi);
-  if (!std::isfinite(hi) || !(std::fabs(hi) >= 1e-30f) || !(std::fabs(hi) <= 1e30f))
+  const float hi = f16 ? round_f16(inv) : round_bf16(inv);
+  const float lo = f16 ? round_f16(inv - hi) : round_bf16(inv - hi);
+  if (!std::isfinite(hi) || !(std::fabs(hi) >= tiny) || !(std::fabs(hi) <= huge))
     return nxa::kFbValu;
-  if (lo != 0.f && !(std::fabs(lo) >= 1e-30f)) return nxa::kFbValu;
+  if (lo != 0.f && !(std::fabs(lo) >= tiny)) return nxa::kFbValu;
   if (d->Lk % 8 != 0 || !aligned(bias, 16) || d->bias_str[0] % 8 != 0 ||
       d->bias_str[1] % 8 != 0)
     return nxa::kFbValu;
@@ -371,10 +395,10 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
   p.ndelta = reinterpret_cast<float*>(wsb + ws.delta);
   p.nlse2 = reinterpret_cast<float*>(
       wsb + ws.delta + align256((size_t)d->B * d->H * d->Lq * sizeof(float)));
-  // bf16: the dQ kernel computes -delta and -lse * log2(e) for its own rows
-  // and runs first; fp32 has a pass of its own.
-  const bool bf16_io = d->io_dtype == NXA_BF16;
-  if (!bf16_io && (rc = launch("delta", stream,
+  // 16-bit I/O: the dQ kernel computes -delta and -lse * log2(e) for its own
+  // rows and runs first; fp32 has a pass of its own.
+  const bool io16 = d->io_dtype != NXA_F32;
+  if (!io16 && (rc = launch("delta", stream,
                                [&] { nxa::launch_delta(p, d->io_dtype, stream); })))
     return rc;
   if (mask) {
@@ -397,13 +421,13 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
     }
   }
   const int dp = d->D <= 64 ? 64 : 128;
-  if (bf16_io &&
+  if (io16 &&
       (rc = launch("dq", stream, [&] { nxa::launch_dq(p, d->io_dtype, dp, stream); })))
     return rc;
   if ((rc = launch("dkdv", stream,
                    [&] { nxa::launch_dkdv(p, d->io_dtype, dp, stream); })))
     return rc;
-  if (!bf16_io &&
+  if (!io16 &&
       (rc = launch("dq", stream, [&] { nxa::launch_dq(p, d->io_dtype, dp, stream); })))
     return rc;
   if (dbias && dg.reduce) {

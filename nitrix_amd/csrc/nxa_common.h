@@ -5,8 +5,9 @@
 // * Tensors are [B, H, L, D] with unit stride over D; the B/H/L strides come
 //   from the descriptor (element units).  Bias and mask are [B, H, Lq, Lk]
 //   with unit stride over Lk and zero strides on broadcast axes.
-// * Matrix products run on 32x32 MFMA tiles (v_mfma_f32_32x32x16_bf16 for
-//   bf16 I/O, v_mfma_f32_32x32x2_f32 for fp32 I/O), fp32 accumulation.
+// * Matrix products run on 32x32 MFMA tiles (v_mfma_f32_32x32x16_bf16 /
+//   _f16 for bf16 / fp16 I/O, v_mfma_f32_32x32x2_f32 for fp32 I/O), fp32
+//   accumulation.
 // * A lane's 16-byte operand chunk c covers head-dim elements
 //   d = c*KC + g*EPC + [0, EPC) where g = lane / 32, EPC = elements per 16 B
 //   and KC = 2*EPC.  A and B operands use the same mapping, so any fixed
@@ -31,6 +32,9 @@ namespace nxa {
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -40,7 +44,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kTile = 64;  // tile-map granularity (queries x keys)
 
-enum DType : int { kBF16 = 0, kF32 = 1 };
+enum DType : int { kBF16 = 0, kF32 = 1, kF16 = 2 };
 
 // dbias handling selected on the host.
 enum DbiasMode : int {
@@ -87,13 +91,14 @@ struct Params {
   int tm_rows;         // mask rows covered by the tile map (Lq, or 1 if broadcast)
   int dbias_mode;
   int dbias_f32;       // 1: dbias points at fp32 partials, else bias dtype
-  int fwd_bias;        // FwdBias mode of the bf16 forward
-  float bias_h, bias_l;  // 1/scale = bias_h + bias_l, both bf16-exact
+  int fwd_bias;        // FwdBias mode of the 16-bit forward
+  float bias_h, bias_l;  // 1/scale = bias_h + bias_l, both exact in the bias dtype
 };
 
-// How the bf16 forward adds the bias (chosen on the host).
+// How the 16-bit forward adds the bias (chosen on the host).
 //  * kFbRow  / kFbTile: the bias enters the score accumulator through MFMA
-//    products bias^T x diag(1/scale) (1/scale split into two bf16 terms), so
+//    products bias^T x diag(1/scale) (1/scale split into two terms of the
+//    bias dtype, which is then the I/O dtype), so
 //    it costs no VALU work; kFbTile streams [query, key] bias tiles through
 //    the LDS ring, kFbRow (bias broadcast over queries) one key row per tile.
 //  * kFbValu: per-element loads and adds (fp32 bias, unaligned layouts).
@@ -114,6 +119,10 @@ struct Mma<bf16> {
                                              const Frag& b) {
     c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
+  // The product alone (accumulator input zero).
+  static __device__ __forceinline__ f32x16 first(const Frag& a, const Frag& b) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, f32x16{}, 0, 0, 0);
+  }
   // Reduction fragment f of a 32-row accumulator block: registers 8f..8f+7
   // (row groups c = 2f, 2f+1).
   static constexpr int FRAGS_PER_BLOCK = 2;
@@ -121,6 +130,28 @@ struct Mma<bf16> {
     Frag r;
 #pragma unroll
     for (int j = 0; j < 8; ++j) r[j] = (bf16)acc[8 * f + j];
+    return r;
+  }
+};
+
+// fp16: the same operand layout as bf16 (8 elements per 16 bytes).
+template <>
+struct Mma<f16> {
+  static constexpr int EPC = 8;
+  static constexpr int KC = 16;
+  using Frag = f16x8;
+  static __device__ __forceinline__ void run(f32x16& c, const Frag& a,
+                                             const Frag& b) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 first(const Frag& a, const Frag& b) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, f32x16{}, 0, 0, 0);
+  }
+  static constexpr int FRAGS_PER_BLOCK = 2;
+  static __device__ __forceinline__ Frag pack(const f32x16& acc, int f) {
+    Frag r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = (f16)acc[8 * f + j];
     return r;
   }
 };
@@ -460,18 +491,22 @@ struct SwzStream {
     for (int m = 0; m < CNT; ++m)
       off[m] = 2u * (uint32_t)(row_of(m, wave, lane) * rs + col_of(m, wave, lane, D));
   }
-  // Copies rows r0.. of `src` into the tile at LDS byte offset `lds`.
-  __device__ __forceinline__ void issue(const bf16* src, int64_t rs, int r0,
+  // Copies rows r0.. of `src` (2-byte elements) into the tile at LDS byte
+  // offset `lds`.
+  template <typename E>
+  __device__ __forceinline__ void issue(const E* src, int64_t rs, int r0,
                                         int nrows, int D, uint32_t lds, int wave,
                                         int lane) const {
 #pragma unroll
     for (int m = 0; m < CNT; ++m) issue_one(src, rs, r0, nrows, D, lds, m, wave, lane);
   }
   // Copy m of the wave's CNT copies of that tile.
-  __device__ __forceinline__ void issue_one(const bf16* src, int64_t rs, int r0,
+  template <typename E>
+  __device__ __forceinline__ void issue_one(const E* src, int64_t rs, int r0,
                                             int nrows, int D, uint32_t lds, int m,
                                             int wave, int lane) const {
-    const bf16* base = src + (int64_t)r0 * rs;  // wave-uniform
+    static_assert(sizeof(E) == 2, "16-bit tiles");
+    const E* base = src + (int64_t)r0 * rs;  // wave-uniform
     if (r0 + 64 <= nrows) {
       dma16_sv(base, off[m], lds + (m * NW + wave) * 1024);
     } else {
@@ -549,6 +584,7 @@ struct PTileCopy {
 };
 
 __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
 __device__ __forceinline__ float to_f32(float x) { return x; }
 
 template <typename T>
@@ -563,6 +599,28 @@ __device__ __forceinline__ void store4(bf16* dst, const f32x16& acc, int off,
 #pragma unroll
   for (int j = 0; j < 4; ++j) v[j] = (bf16)(acc[off + j] * scale);
   *reinterpret_cast<bf16x4*>(dst) = v;
+}
+__device__ __forceinline__ void store4(f16* dst, const f32x16& acc, int off,
+                                       float scale) {
+  f16x4 v;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = (f16)(acc[off + j] * scale);
+  *reinterpret_cast<f16x4*>(dst) = v;
+}
+
+// One bias / dbias element of runtime dtype `dt` (kBF16, kF16 or kF32).
+__device__ __forceinline__ float load_elem(int dt, const void* base, int64_t off) {
+  if (dt == kBF16) return (float)reinterpret_cast<const bf16*>(base)[off];
+  if (dt == kF16) return (float)reinterpret_cast<const f16*>(base)[off];
+  return reinterpret_cast<const float*>(base)[off];
+}
+__device__ __forceinline__ void store_elem(int dt, void* base, int64_t off, float x) {
+  if (dt == kBF16)
+    reinterpret_cast<bf16*>(base)[off] = (bf16)x;
+  else if (dt == kF16)
+    reinterpret_cast<f16*>(base)[off] = (f16)x;
+  else
+    reinterpret_cast<float*>(base)[off] = x;
 }
 __device__ __forceinline__ void store4(float* dst, const f32x16& acc, int off,
                                        float scale) {
@@ -580,6 +638,17 @@ __device__ __forceinline__ f32x4 load_bias4(const Params& p, const void* base,
     const bf16* b = reinterpret_cast<const bf16*>(base) + off;
     if (p.bias_vec && valid >= 4) {
       const bf16x4 v = *reinterpret_cast<const bf16x4*>(b);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r[j] = (float)v[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j < valid) r[j] = (float)b[j];
+    }
+  } else if (p.bias_dtype == kF16) {
+    const f16* b = reinterpret_cast<const f16*>(base) + off;
+    if (p.bias_vec && valid >= 4) {
+      const f16x4 v = *reinterpret_cast<const f16x4*>(b);
 #pragma unroll
       for (int j = 0; j < 4; ++j) r[j] = (float)v[j];
     } else {

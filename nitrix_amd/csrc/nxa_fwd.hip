@@ -75,7 +75,7 @@ __global__ __launch_bounds__(256) void tilemap_kernel(const Params p, int MB,
 }
 
 // ---------------------------------------------------------------------------
-// Forward kernel (fp32 I/O; bf16 I/O has its own kernel with direct
+// Forward kernel (fp32 I/O; 16-bit I/O has its own kernel with direct
 // global->LDS tile copies).  Block = 4 waves x 32 queries (128 rows); two blocks share
 // a CU, so one block's softmax (VALU, v_exp) overlaps the other's MFMAs.
 // 64-key K/V tiles stream through double-buffered LDS: the next tile is
@@ -369,8 +369,8 @@ static void launch_fwd_flags(const Params& p, hipStream_t stream) {
 }
 
 void launch_fwd(const Params& p, int io_dtype, int dp, hipStream_t stream) {
-  if (io_dtype == kBF16) {
-    launch_fwd_bf16(p, dp, stream);
+  if (io_dtype == kBF16 || io_dtype == kF16) {
+    launch_fwd16(p, io_dtype, dp, stream);
   } else {
     if (dp == 64) launch_fwd_flags<float, 64>(p, stream);
     else launch_fwd_flags<float, 128>(p, stream);

@@ -1,5 +1,7 @@
-// bf16 forward kernel for gfx950: fused flash-attention forward with an
-// online softmax in base 2 and an fp32 log-sum-exp per query row.
+// 16-bit (bf16 / fp16 I/O) forward kernel for gfx950: fused flash-attention
+// forward with an online softmax in base 2 and an fp32 log-sum-exp per query
+// row.  Both element types share the code: the MFMA (bf16 or f16 32x32x16)
+// and the conversions follow the template type T.
 //
 // Same math as the reference's forward Pallas kernel
 // (src/nitrix/_kernels/cuda/attention.py:85-156): logits = scale * Q K^T +
@@ -27,9 +29,10 @@
 // enters the score accumulator as MFMA products before Q K^T accumulates on
 // top: S^T += bias^T x diag(1/scale), so S^T = K Q^T + bias / scale and the
 // exponent's FMA by scale*log2(e) yields the logits of the reference.  1/scale
-// is split into two bf16 terms h + l (l = 0 when 1/scale is a power of two,
-// e.g. D = 64), so the bias contributes bias * (h + l) * scale = bias to
-// within 2^-16 relative.
+// is split into two terms h + l of the bias dtype, which these modes require
+// to be T (l = 0 when 1/scale is a power of two, e.g. D = 64), so the bias
+// contributes bias * (h + l) * scale = bias to within 2^-16 relative (bf16;
+// 2^-22 for fp16).
 //  * Full bias tiles (kFbTile, [query, key] rows of 64 keys): a ring of its
 //    own holds the block's [256 x 64] bias tiles (XOR-swizzled, filled by
 //    direct copies, 8 contiguous 128-byte rows per copy, each wave its own
@@ -100,10 +103,10 @@ struct FwdRing {
 // NW waves of 32 queries per block: 8 (ping-pong pairs on each SIMD, one
 // block per CU) or 4 (two blocks per CU; for masks that vary over queries, so
 // that a block's key-tile list is that of its own 128 rows).
-template <int DP, int NW, int BMODE, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
-  using M = Mma<bf16>;
-  using Frag = bf16x8;
+template <typename T, int DP, int NW, int BMODE, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64, 2) void fwd16_kernel(const Params p) {
+  using M = Mma<T>;
+  using Frag = typename M::Frag;
   constexpr int EPC = 8, KC = 16;
   constexpr int BM = NW * 32, BN = 64;
   using R = FwdRing<DP, NW, BMODE>;
@@ -124,8 +127,8 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
   constexpr int BT_COPIES = BMODE == kFbTile ? 4 : 0;
   // Copies each wave issues per tile into the K / V ring.
   constexpr int KV_COPIES = 2 * KS::CNT + (BMODE == kFbRow ? 1 : 0);
-  __shared__ __attribute__((aligned(16))) bf16 ring[NST * STAGE_ELEMS];
-  __shared__ __attribute__((aligned(16))) bf16 bring[NSTB * BT_ELEMS];
+  __shared__ __attribute__((aligned(16))) T ring[NST * STAGE_ELEMS];
+  __shared__ __attribute__((aligned(16))) T bring[NSTB * BT_ELEMS];
   __shared__ uint16_t act[kFwdMaxTiles];  // active key tiles, in order
   __shared__ uint8_t acls[kFwdMaxTiles];  // their classes
   __shared__ int nact_s;
@@ -143,8 +146,8 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
   const bool qok = qrow < p.Lq;
   const int qc = qok ? qrow : p.Lq - 1;
 
-  const bf16* kp = (const bf16*)p.k + b * p.k_str[0] + h * p.k_str[1];
-  const bf16* vp = (const bf16*)p.v + b * p.v_str[0] + h * p.v_str[1];
+  const T* kp = (const T*)p.k + b * p.k_str[0] + h * p.k_str[1];
+  const T* vp = (const T*)p.v + b * p.v_str[0] + h * p.v_str[1];
   const int64_t ks = p.k_str[2], vs = p.v_str[2];
 
   // --- active key tiles of this block (tile-map classes) --------------------
@@ -185,12 +188,12 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
   // --- stationary Q^T fragments ----------------------------------------------
   Frag qf[NC];
   {
-    const bf16* qp = (const bf16*)p.q + b * p.q_str[0] + h * p.q_str[1] +
+    const T* qp = (const T*)p.q + b * p.q_str[0] + h * p.q_str[1] +
                      (int64_t)qrow * p.q_str[2];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int d = c * KC + g * EPC;
-      qf[c] = (qok && d < p.D) ? ld16(qp + d) : zero_frag<bf16>();
+      qf[c] = (qok && d < p.D) ? ld16(qp + d) : zero_frag<T>();
     }
   }
   const int64_t brow = VALU_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] +
@@ -213,16 +216,16 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const bool on = 16 * f + 8 * (e >> 2) + 4 * g + (e & 3) == c32;
-        bdh[f][e] = (bf16)(on ? p.bias_h : 0.f);
-        bdl[f][e] = (bf16)(on ? p.bias_l : 0.f);
+        bdh[f][e] = (T)(on ? p.bias_h : 0.f);
+        bdl[f][e] = (T)(on ? p.bias_l : 0.f);
       }
   } else if constexpr (BMODE == kFbRow) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const bool on = g == 0 && e == 0;
-      bdh[0][e] = (bf16)(on ? p.bias_h : 0.f);
-      bdl[0][e] = (bf16)(on ? p.bias_l : 0.f);
-      bdh[1][e] = bdl[1][e] = (bf16)0.f;
+      bdh[0][e] = (T)(on ? p.bias_h : 0.f);
+      bdl[0][e] = (T)(on ? p.bias_l : 0.f);
+      bdh[1][e] = bdl[1][e] = (T)0.f;
     }
   }
 
@@ -252,7 +255,7 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
   // Row bias: lane l copies keys 2(l%32), 2(l%32)+1 of the row.
   // Offsets are relative to the wave's first row (32 rows times the row
   // stride fit in 32 bits: the host bounds the stride).
-  const bf16* bp = (const bf16*)p.bias;
+  const T* bp = (const T*)p.bias;  // MFMA bias modes: bias dtype is T
   uint32_t boff[BT_COPIES > 0 ? BT_COPIES : 1];
   if constexpr (MFMA_BIAS) bp += b * p.bias_str[0] + h * p.bias_str[1];
   auto bias_chunk = [&](int m) NXA_INLINE -> int {
@@ -389,7 +392,7 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
         for (int f = 0; f < 2; ++f) {
           const Frag a = tr_frag(b0 + f * (16 * 128), b1 + f * (16 * 128));
           if (f == 0)
-            S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bdh[f], f32x16{}, 0, 0, 0);
+            S[kb] = M::first(a, bdh[f]);
           else
             M::run(S[kb], a, bdh[f]);
           if (bias_l) M::run(S[kb], a, bdl[f]);
@@ -397,13 +400,13 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
       }
       fresh = false;
     } else if constexpr (BMODE == kFbRow) {
-      const bf16* Bs = ring + (i % NST) * STAGE_ELEMS + 2 * TILE_ELEMS + wave * 128;
+      const T* Bs = ring + (i % NST) * STAGE_ELEMS + 2 * TILE_ELEMS + wave * 128;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        Frag a = zero_frag<bf16>();
-        const bf16 bv = Bs[kb * 32 + c32];
-        a[0] = g == 0 ? bv : (bf16)0.f;
-        S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bdh[0], f32x16{}, 0, 0, 0);
+        Frag a = zero_frag<T>();
+        const T bv = Bs[kb * 32 + c32];
+        a[0] = g == 0 ? bv : (T)0.f;
+        S[kb] = M::first(a, bdh[0]);
         if (bias_l) M::run(S[kb], a, bdl[0]);
       }
       fresh = false;
@@ -414,8 +417,7 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
 #pragma unroll
     for (int j = 0; j < 2 * NC; ++j) {
       if (fresh && j < 2)
-        S[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kbuf[j % PD], qf[j >> 1],
-                                                           f32x16{}, 0, 0, 0);
+        S[j & 1] = M::first(kbuf[j % PD], qf[j >> 1]);
       else
         M::run(S[j & 1], kbuf[j % PD], qf[j >> 1]);
       if (j + PD < 2 * NC) kbuf[j % PD] = kfrag(j + PD);
@@ -505,7 +507,7 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
   };
-  // P block kb = exp2(S[kb] cc - m_ref), packed to the bf16 reduction
+  // P block kb = exp2(S[kb] cc - m_ref), packed to the T reduction
   // fragments of P V; its row sum (four chains) joins l.
   Frag pf[2][FPB];
   auto exp_half = [&](int kb, float cc) NXA_INLINE {
@@ -639,7 +641,7 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
   const float l = l_i + shfl_xor32(l_i);
   const float inv = 1.0f / l;
   if (qok) {
-    bf16* op = (bf16*)p.o + b * p.o_str[0] + h * p.o_str[1] + (int64_t)qrow * p.o_str[2];
+    T* op = (T*)p.o + b * p.o_str[0] + h * p.o_str[1] + (int64_t)qrow * p.o_str[2];
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -652,48 +654,54 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_bf16_kernel(const Params p) {
   }
 }
 
-template <int DP, int NW, int BMODE, bool CA>
-static void launch_fwd_bf16_t(Params p, hipStream_t stream) {
+template <typename T, int DP, int NW, int BMODE, bool CA>
+static void launch_fwd16_t(Params p, hipStream_t stream) {
   constexpr int BM = NW * 32;
   p.nqt = (p.Lq + BM - 1) / BM;
   const int n = p.B * p.H * p.nqt;
-  hipLaunchKernelGGL((fwd_bf16_kernel<DP, NW, BMODE, CA>), dim3(n), dim3(NW * 64), 0, stream,
+  hipLaunchKernelGGL((fwd16_kernel<T, DP, NW, BMODE, CA>), dim3(n), dim3(NW * 64), 0, stream,
                      p);
 }
 
-template <int DP, int NW, int BMODE>
-static void launch_fwd_bf16_c(const Params& p, hipStream_t stream) {
-  if (p.causal) launch_fwd_bf16_t<DP, NW, BMODE, true>(p, stream);
-  else launch_fwd_bf16_t<DP, NW, BMODE, false>(p, stream);
+template <typename T, int DP, int NW, int BMODE>
+static void launch_fwd16_c(const Params& p, hipStream_t stream) {
+  if (p.causal) launch_fwd16_t<T, DP, NW, BMODE, true>(p, stream);
+  else launch_fwd16_t<T, DP, NW, BMODE, false>(p, stream);
 }
 
 // 4-wave blocks when the mask varies over queries (its tile map has rows) at
 // D <= 64, where two such blocks (4 K / V stages each) share a CU's LDS;
 // full bias tiles keep the 8-wave block, whose bias ring they need.
-template <int DP, int BMODE>
-static void launch_fwd_bf16_nw(const Params& p, hipStream_t stream) {
+template <typename T, int DP, int BMODE>
+static void launch_fwd16_nw(const Params& p, hipStream_t stream) {
   if constexpr (DP == 64 && BMODE != kFbTile) {
     if (p.has_tilemap && p.tm_rows > 1) {
-      launch_fwd_bf16_c<DP, 4, BMODE>(p, stream);
+      launch_fwd16_c<T, DP, 4, BMODE>(p, stream);
       return;
     }
   }
-  launch_fwd_bf16_c<DP, 8, BMODE>(p, stream);
+  launch_fwd16_c<T, DP, 8, BMODE>(p, stream);
 }
 
-template <int DP>
-static void launch_fwd_bf16_flags(const Params& p, hipStream_t stream) {
+template <typename T, int DP>
+static void launch_fwd16_flags(const Params& p, hipStream_t stream) {
   switch (p.has_bias ? p.fwd_bias : kFbNone) {
-    case kFbRow: launch_fwd_bf16_nw<DP, kFbRow>(p, stream); break;
-    case kFbTile: launch_fwd_bf16_nw<DP, kFbTile>(p, stream); break;
-    case kFbValu: launch_fwd_bf16_nw<DP, kFbValu>(p, stream); break;
-    default: launch_fwd_bf16_nw<DP, kFbNone>(p, stream); break;
+    case kFbRow: launch_fwd16_nw<T, DP, kFbRow>(p, stream); break;
+    case kFbTile: launch_fwd16_nw<T, DP, kFbTile>(p, stream); break;
+    case kFbValu: launch_fwd16_nw<T, DP, kFbValu>(p, stream); break;
+    default: launch_fwd16_nw<T, DP, kFbNone>(p, stream); break;
   }
 }
 
-void launch_fwd_bf16(const Params& p, int dp, hipStream_t stream) {
-  if (dp == 64) launch_fwd_bf16_flags<64>(p, stream);
-  else launch_fwd_bf16_flags<128>(p, stream);
+template <typename T>
+static void launch_fwd16_dp(const Params& p, int dp, hipStream_t stream) {
+  if (dp == 64) launch_fwd16_flags<T, 64>(p, stream);
+  else launch_fwd16_flags<T, 128>(p, stream);
+}
+
+void launch_fwd16(const Params& p, int io_dtype, int dp, hipStream_t stream) {
+  if (io_dtype == kF16) launch_fwd16_dp<f16>(p, dp, stream);
+  else launch_fwd16_dp<bf16>(p, dp, stream);
 }
 
 }  // namespace nxa

@@ -10,12 +10,12 @@ namespace nxa {
 void launch_tilemap(const Params& p, int MB, int MH, int MQ, int MK, int vec16,
                     hipStream_t stream);
 void launch_fwd(const Params& p, int io_dtype, int dp, hipStream_t stream);
-void launch_fwd_bf16(const Params& p, int dp, hipStream_t stream);
+void launch_fwd16(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_delta(const Params& p, int io_dtype, hipStream_t stream);
 void launch_dkdv(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream);
-void launch_dkdv_bf16(const Params& p, int dp, hipStream_t stream);
-void launch_dq_bf16(const Params& p, int dp, hipStream_t stream);
+void launch_dkdv16(const Params& p, int io_dtype, int dp, hipStream_t stream);
+void launch_dq16(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dbias_reduce(const Params& p, void* out, const int64_t* out_str,
                          int OB, int OH, int LQ, hipStream_t stream);
 

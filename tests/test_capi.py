@@ -69,6 +69,19 @@ def _check(lib, d, has_bias=1, has_mask=1):
 def test_valid_descriptor(lib):
     assert _check(lib, _desc()) == _lib.NXA_OK
     assert _check(lib, _desc(dtype=_lib.NXA_F32, D=12)) == _lib.NXA_OK
+    assert _check(lib, _desc(dtype=_lib.NXA_F16, D=40)) == _lib.NXA_OK
+
+
+def test_fp16_head_dim_multiple_of_8(lib):
+    d = _desc(dtype=_lib.NXA_F16, D=12)
+    assert _check(lib, d) == _lib.NXA_E_UNSUPPORTED
+    assert 'multiple of 8' in lib.nxa_last_error().decode()
+
+
+def test_mixed_bias_dtype_is_valid(lib):
+    d = _desc(dtype=_lib.NXA_F16)
+    d.bias_dtype = _lib.NXA_BF16
+    assert _check(lib, d) == _lib.NXA_OK
 
 
 @pytest.mark.parametrize(

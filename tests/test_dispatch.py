@@ -141,7 +141,9 @@ def test_validate_raises_value_error(shapes):
         (torch.bfloat16, 128, 128, True),
         (torch.bfloat16, 40, 40, True),
         (torch.float32, 12, 12, True),
-        (torch.float16, 64, 64, False),
+        (torch.float16, 64, 64, True),
+        (torch.float16, 24, 24, True),
+        (torch.float16, 12, 12, False),
         (torch.float64, 64, 64, False),
         (torch.bfloat16, 64, 32, False),
         (torch.bfloat16, 136, 136, False),

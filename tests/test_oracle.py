@@ -277,6 +277,39 @@ def test_round_bf16_matches_torch():
     np.testing.assert_array_equal(O.round_bf16(x), want)
 
 
+def test_round_f16_matches_torch():
+    torch = pytest.importorskip('torch')
+    rng = np.random.RandomState(1)
+    x = np.concatenate(
+        [
+            rng.standard_normal(10000).astype(np.float32) * 100,
+            rng.standard_normal(1000).astype(np.float32) * 1e-6,  # subnormal halves
+            np.array([0.0, -0.0, np.inf, -np.inf, 7e4, -7e4, 65519.0, 1e-9], np.float32),
+        ]
+    )
+    want = torch.from_numpy(x).to(torch.float16).float().numpy()
+    np.testing.assert_array_equal(O.round_f16(x), want)
+
+
+def test_round_f16_known_answers():
+    # ulp(1) = 2^-10: 1 + 2^-11 is a tie (to the even 1.0), 1 + 3 * 2^-11 a
+    # tie to the even 1 + 2^-9; 65504 is the largest half, 65520 the first
+    # value that rounds to inf; 2^-24 is the smallest subnormal.
+    x = np.array([1 + 2.0**-11, 1 + 3 * 2.0**-11, 65519.0, 65520.0,
+                  2.0**-25, 3 * 2.0**-26, 2.0**-14 + 2.0**-25], np.float32)
+    want = np.array([1.0, 1 + 2.0**-9, 65504.0, np.inf, 0.0, 2.0**-24, 2.0**-14],
+                    np.float32)
+    np.testing.assert_array_equal(O.round_f16(x), want)
+
+
+def test_f16_invariant_is_fp32_path_on_rounded_inputs():
+    d = load_golden('attention_dense_float32')
+    qh, kh, vh = (O.round_f16(d[n]) for n in ('q', 'k', 'v'))
+    out = O.round_f16(O.sdpa_forward(qh, kh, vh))
+    atol, rtol = TOL[('attention', 'float16')]
+    np.testing.assert_allclose(out, d['out'], atol=atol, rtol=rtol)
+
+
 def test_bf16_invariant_is_fp32_path_on_rounded_inputs():
     # reduced-precision reference == fp32 path on the bf16 inputs, cast back.
     d = load_golden('attention_dense_float32')
