@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define NXA_VERSION 1
+#define NXA_VERSION 2
 
 typedef enum { NXA_BF16 = 0, NXA_F32 = 1, NXA_F16 = 2 } nxa_dtype;
 
@@ -65,7 +65,8 @@ enum {
 };
 
 typedef struct {
-  int32_t B, H, Lq, Lk, D;  /* D <= 128, D % 8 == 0 (bf16, fp16) or % 4 (fp32) */
+  int32_t B, H, Lq, Lk, D;  /* head dim of q, k; D <= 128, D % 8 == 0 (bf16,
+                               fp16) or % 4 (fp32)                            */
   int32_t io_dtype;         /* nxa_dtype of q, k, v, o, dO, dq, dk, dv       */
   int32_t bias_dtype;       /* nxa_dtype of bias and dbias                   */
   int32_t causal;           /* nonzero: keep key j for query i iff j <= i    */
@@ -76,6 +77,7 @@ typedef struct {
   int64_t o_str[3];         /* B, H, Lq strides of o (and dO)                */
   int64_t bias_str[3];      /* B, H, Lq strides of bias; 0 = broadcast       */
   int64_t mask_str[3];      /* B, H, Lq strides of mask; 0 = broadcast       */
+  int32_t Dv;               /* head dim of v, o (dO, dv); 0 = D; same limits  */
 } nxa_desc;
 
 /* Library version (NXA_VERSION of the build). */

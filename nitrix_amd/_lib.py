@@ -72,6 +72,7 @@ class NxaDesc(ctypes.Structure):
         ('o_str', _I64x3),
         ('bias_str', _I64x3),
         ('mask_str', _I64x3),
+        ('Dv', ctypes.c_int32),
     ]
 
 

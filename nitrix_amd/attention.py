@@ -159,9 +159,10 @@ def reference_scaled_dot_product_attention(
 def _check_tileable(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
     """Reject shapes the gfx950 kernels cannot run (``attention.py:708-765``).
 
-    Accepts bf16, fp16 or fp32 (q, k, v of one dtype), ``d_v == d``, head dim
-    up to 128 (a multiple of 8 for the 16-bit types, of 4 for fp32) and any
-    positive query / key lengths (tails are predicated in the kernels).
+    Accepts bf16, fp16 or fp32 (q, k, v of one dtype), head dims ``d`` (q, k)
+    and ``d_v`` (v) up to 128 each (multiples of 8 for the 16-bit types, of 4
+    for fp32) and any positive query / key lengths (tails are predicated in
+    the kernels).
     """
     if q.dtype not in _IO_DTYPES:
         raise HipNotTileable(
@@ -173,17 +174,14 @@ def _check_tileable(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
             f'{k.dtype}, {v.dtype}.'
         )
     d, d_v = q.shape[-1], v.shape[-1]
-    if d_v != d:
-        raise HipNotTileable(
-            f'fused attention requires d_v == d; got d={d}, d_v={d_v}.'
-        )
     epc = 4 if q.dtype == torch.float32 else 8
-    if d > _MAX_HEAD_DIM or d % epc != 0:
-        raise HipNotTileable(
-            f'fused attention requires head dim <= {_MAX_HEAD_DIM} and a '
-            f'multiple of {epc}; got {d}.'
-        )
-    if q.shape[-2] == 0 or k.shape[-2] == 0 or d == 0:
+    for name, n in (('d', d), ('d_v', d_v)):
+        if n > _MAX_HEAD_DIM or n % epc != 0:
+            raise HipNotTileable(
+                f'fused attention requires head dims <= {_MAX_HEAD_DIM} and '
+                f'multiples of {epc}; got {name}={n}.'
+            )
+    if q.shape[-2] == 0 or k.shape[-2] == 0 or d == 0 or d_v == 0:
         raise HipNotTileable('fused attention needs non-empty q / k / v.')
     if not (q.device == k.device == v.device):
         raise HipNotTileable('q, k, v are on different devices.')
@@ -242,6 +240,7 @@ class _Prepared:
         self.h = lead[-1]
         self.nb = int(math.prod(self.batch)) if self.batch else 1
         self.s, self.t, self.d = s, t, d
+        self.dv = v.shape[-1]
         self.dtype = q.dtype
         self.device = q.device
         self.epc = 4 if q.dtype == torch.float32 else 8
@@ -265,6 +264,7 @@ class _Prepared:
 
         desc = _lib.NxaDesc()
         desc.B, desc.H, desc.Lq, desc.Lk, desc.D = self.nb, self.h, s, t, d
+        desc.Dv = self.dv
         desc.io_dtype = _IO_DTYPES[q.dtype]
         desc.bias_dtype = (
             _BIAS_DTYPES[self.bias.dtype] if self.bias is not None else _lib.NXA_F32
@@ -275,7 +275,8 @@ class _Prepared:
         desc.k_str[:] = self.k.stride()[:3]
         desc.v_str[:] = self.v.stride()[:3]
         # outputs are allocated contiguous
-        desc.o_str[:] = (self.h * s * d, s * d, d)
+        dv = self.dv
+        desc.o_str[:] = (self.h * s * dv, s * dv, dv)
         if self.bias is not None:
             desc.bias_str[:] = self.bias.stride()[:3]
         if self.mask is not None:
@@ -312,7 +313,7 @@ def _forward(prep: _Prepared, for_bwd: bool = False):
     starts with the forward's tile map), so the backward reuses it as is."""
     lib = _lib.lib()
     o = torch.empty(
-        (prep.nb, prep.h, prep.s, prep.d), dtype=prep.dtype, device=prep.device
+        (prep.nb, prep.h, prep.s, prep.dv), dtype=prep.dtype, device=prep.device
     )
     lse = torch.empty(
         (prep.nb, prep.h, prep.s), dtype=torch.float32, device=prep.device
@@ -355,7 +356,7 @@ def _backward(prep: _Prepared, o, lse, fwd_ws, dout, want_dbias: bool):
         prep.desc.q_str[:] = q.stride()[:3]
         prep.desc.k_str[:] = k.stride()[:3]
         prep.desc.v_str[:] = v.stride()[:3]
-    dout = dout.reshape(prep.nb, prep.h, prep.s, prep.d)
+    dout = dout.reshape(prep.nb, prep.h, prep.s, prep.dv)
     if not dout.is_contiguous() or dout.data_ptr() % 16 != 0:
         dout = dout.contiguous()
     dq = torch.empty_like(q, memory_format=torch.contiguous_format)
@@ -425,7 +426,7 @@ class _SdpaHip(torch.autograd.Function):
         ctx.prep = prep
         ctx.shapes = (tuple(q.shape), tuple(k.shape), tuple(v.shape))
         ctx.save_for_backward(o, lse, ws if ws is not None else torch.empty(0))
-        return o.reshape(*prep.lead, prep.s, prep.d)
+        return o.reshape(*prep.lead, prep.s, prep.dv)
 
     @staticmethod
     def backward(ctx, dout):
@@ -439,7 +440,7 @@ class _SdpaHip(torch.autograd.Function):
         lead = prep.lead
         dq = _unbroadcast(dq.reshape(*lead, prep.s, prep.d), qs)
         dk = _unbroadcast(dk.reshape(*lead, prep.t, prep.d), ks)
-        dv = _unbroadcast(dv.reshape(*lead, prep.t, prep.d), vs)
+        dv = _unbroadcast(dv.reshape(*lead, prep.t, prep.dv), vs)
         dbias = None
         if dbias_k is not None:
             ob, oh, lq = dbias_k.shape[:3]

@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256) void delta_kernel(const Params p) {
     const int64_t off = b * p.o_str[0] + h * p.o_str[1] + (int64_t)q * p.o_str[2];
     const T* o = (const T*)p.o + off;
     const T* d = (const T*)p.dout + off;
-    for (int c = sub * EPC; c < p.D; c += 16 * EPC) {
+    for (int c = sub * EPC; c < p.Dv; c += 16 * EPC) {
       const Frag x = ld16(o + c), y = ld16(d + c);
 #pragma unroll
       for (int j = 0; j < EPC; ++j) acc += to_f32(x[j]) * to_f32(y[j]);
@@ -150,9 +150,8 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int d = c * KC + g * EPC;
-    const bool ok = kok && d < p.D;
-    kf[c] = ok ? ld16(kp + (int64_t)key * p.k_str[2] + d) : zero_frag<T>();
-    vf[c] = ok ? ld16(vp + (int64_t)key * p.v_str[2] + d) : zero_frag<T>();
+    kf[c] = kok && d < p.D ? ld16(kp + (int64_t)key * p.k_str[2] + d) : zero_frag<T>();
+    vf[c] = kok && d < p.Dv ? ld16(vp + (int64_t)key * p.v_str[2] + d) : zero_frag<T>();
   }
   f32x16 dk[NDB], dv[NDB];
 #pragma unroll
@@ -189,7 +188,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
     }
     __syncthreads();
     load_tile<T, DP, BQ, SK, ST, true>(qp, p.q_str[2], q0, p.Lq, p.D, Qs, Qt, tid);
-    load_tile<T, DP, BQ, SK, ST, true>(dop, p.o_str[2], q0, p.Lq, p.D, Ds, Dt, tid);
+    load_tile<T, DP, BQ, SK, ST, true>(dop, p.o_str[2], q0, p.Lq, p.Dv, Ds, Dt, tid);
     if (tid < BQ) {
       const int q = q0 + tid;
       lse_s[tid] = q < p.Lq ? lsep[q] * kLog2e : 0.f;
@@ -264,12 +263,10 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int d0 = db * 32 + 8 * c + 4 * g;
-        if (d0 < p.D) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            dkp[d0 + j] = from_f32<T>(dk[db][4 * c + j] * p.scale);
-            dvp[d0 + j] = from_f32<T>(dv[db][4 * c + j]);
-          }
+        for (int j = 0; j < 4; ++j) {
+          if (d0 < p.D) dkp[d0 + j] = from_f32<T>(dk[db][4 * c + j] * p.scale);
+          if (d0 < p.Dv) dvp[d0 + j] = from_f32<T>(dv[db][4 * c + j]);
         }
       }
   }
@@ -320,9 +317,8 @@ __global__ __launch_bounds__(256) void dq_kernel(const Params p) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int d = c * KC + g * EPC;
-    const bool ok = qok && d < p.D;
-    qf[c] = ok ? ld16(qp + (int64_t)qrow * p.q_str[2] + d) : zero_frag<T>();
-    df[c] = ok ? ld16(dop + (int64_t)qrow * p.o_str[2] + d) : zero_frag<T>();
+    qf[c] = qok && d < p.D ? ld16(qp + (int64_t)qrow * p.q_str[2] + d) : zero_frag<T>();
+    df[c] = qok && d < p.Dv ? ld16(dop + (int64_t)qrow * p.o_str[2] + d) : zero_frag<T>();
   }
   const int64_t rowid = ((int64_t)b * p.H + h) * p.Lq + qclamp;
   const float lse2 = p.lse[rowid] * kLog2e;
@@ -353,7 +349,7 @@ __global__ __launch_bounds__(256) void dq_kernel(const Params p) {
     if (!(cls & 1)) continue;
     __syncthreads();
     load_tile<T, DP, BN, SK, ST, true>(kp, p.k_str[2], k0, p.Lk, p.D, Ks, Kt, tid);
-    load_tile<T, DP, BN, SK, ST, false>(vp, p.v_str[2], k0, p.Lk, p.D, Vs, nullptr, tid);
+    load_tile<T, DP, BN, SK, ST, false>(vp, p.v_str[2], k0, p.Lk, p.Dv, Vs, nullptr, tid);
     __syncthreads();
 
     f32x16 s[2], dp[2];

@@ -160,7 +160,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int d = c * KC + g * EPC;
-      bfr[c] = (kok && d < p.D) ? ld16(src + d) : zero_frag<T>();
+      bfr[c] = (kok && d < (pw ? p.D : p.Dv)) ? ld16(src + d) : zero_frag<T>();
     }
   }
   f32x16 acc[NDB];  // dV^T (P wave) or dK^T (dS wave)
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
   const int cw = wave & 3;
   QS qsm, dsm;
   qsm.init(qs, p.D, cw, lane);
-  dsm.init(os, p.D, cw, lane);
+  dsm.init(os, p.Dv, cw, lane);
   const uint32_t lds0 = lds_offset(smem);
   const uint32_t pbuf = lds0 + NST * STAGE_BYTES;
   struct TileSrc {
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
     s.q = make_rsrc(qp + (int64_t)q0 * qs,
                     left > 0 ? (uint32_t)(((int64_t)(left - 1) * qs + p.D) * 2) : 0u);
     s.d = make_rsrc(dop + (int64_t)q0 * os,
-                    left > 0 ? (uint32_t)(((int64_t)(left - 1) * os + p.D) * 2) : 0u);
+                    left > 0 ? (uint32_t)(((int64_t)(left - 1) * os + p.Dv) * 2) : 0u);
     s.r = make_rsrc((cw == 0 ? nlp : ndp) + q0, (uint32_t)max(left, 0) * 4u);
     return s;
   };
@@ -508,7 +508,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int d0 = db * 32 + 8 * c + 4 * g;
-          if (d0 < p.D) store4(dvp + d0, acc[db], 4 * c, 1.0f);
+          if (d0 < p.Dv) store4(dvp + d0, acc[db], 4 * c, 1.0f);
         }
     }
   }
@@ -612,9 +612,8 @@ __global__ __launch_bounds__(256, 2) void dq16_kernel(const Params p) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int d = c * KC + g * EPC;
-      const bool ok = qok && d < p.D;
-      qf[c] = ok ? ld16(qp + d) : zero_frag<T>();
-      df[c] = ok ? ld16(dop + d) : zero_frag<T>();
+      qf[c] = qok && d < p.D ? ld16(qp + d) : zero_frag<T>();
+      df[c] = qok && d < p.Dv ? ld16(dop + d) : zero_frag<T>();
     }
   }
   // Per-row values of the backward, computed here for this block's rows
@@ -629,7 +628,7 @@ __global__ __launch_bounds__(256, 2) void dq16_kernel(const Params p) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int d = c * KC + g * EPC;
-      const Frag of = (qok && d < p.D) ? ld16(op + d) : zero_frag<T>();
+      const Frag of = (qok && d < p.Dv) ? ld16(op + d) : zero_frag<T>();
 #pragma unroll
       for (int e = 0; e < EPC; ++e) dacc = __builtin_fmaf((float)of[e], (float)df[c][e], dacc);
     }
@@ -685,7 +684,7 @@ __global__ __launch_bounds__(256, 2) void dq16_kernel(const Params p) {
   // --- copies --------------------------------------------------------------------
   KS ksm, vsm;
   ksm.init(ks, p.D, wave, lane);
-  vsm.init(vs, p.D, wave, lane);
+  vsm.init(vs, p.Dv, wave, lane);
   const uint32_t lds0 = lds_offset(smem);
   const T* bp = ROW_BIAS ? (const T*)p.bias + b * p.bias_str[0] + h * p.bias_str[1]
                          : nullptr;
@@ -701,7 +700,7 @@ __global__ __launch_bounds__(256, 2) void dq16_kernel(const Params p) {
     s.k = make_rsrc(kp + (int64_t)k0 * ks,
                     left > 0 ? (uint32_t)(((int64_t)(left - 1) * ks + p.D) * 2) : 0u);
     s.v = make_rsrc(vp + (int64_t)k0 * vs,
-                    left > 0 ? (uint32_t)(((int64_t)(left - 1) * vs + p.D) * 2) : 0u);
+                    left > 0 ? (uint32_t)(((int64_t)(left - 1) * vs + p.Dv) * 2) : 0u);
     if constexpr (ROW_BIAS)
       s.r = make_rsrc(bp + k0, (uint32_t)max(left, 0) * 2u);
     return s;

@@ -34,6 +34,15 @@ int esize(int dt) { return dt == NXA_F32 ? 4 : 2; }
 
 bool known_dtype(int dt) { return dt == NXA_BF16 || dt == NXA_F32 || dt == NXA_F16; }
 
+// Head dim of v / o (Dv = 0 means Dv = D).
+int value_dim(const nxa_desc* d) { return d->Dv > 0 ? d->Dv : d->D; }
+
+// Padded head-dim width the kernels are instantiated for.
+int padded_dim(const nxa_desc* d) {
+  const int m = d->D > value_dim(d) ? d->D : value_dim(d);
+  return m <= 64 ? 64 : 128;
+}
+
 // ---------------------------------------------------------------------------
 // Profiling: HIP events around each launch while enabled.
 // ---------------------------------------------------------------------------
@@ -86,11 +95,16 @@ int check_desc(const nxa_desc* d, int has_bias, int has_mask) {
     return fail(NXA_E_SHAPE, "extents must be positive (B=%d H=%d Lq=%d Lk=%d D=%d)",
                 d->B, d->H, d->Lq, d->Lk, d->D);
   const int epc = 16 / esize(d->io_dtype);
-  if (d->D > 128)
-    return fail(NXA_E_UNSUPPORTED, "head dim D=%d exceeds 128", d->D);
-  if (d->D % epc != 0)
-    return fail(NXA_E_UNSUPPORTED, "head dim D=%d must be a multiple of %d",
-                d->D, epc);
+  if (d->Dv < 0) return fail(NXA_E_SHAPE, "value head dim Dv=%d is negative", d->Dv);
+  const int dims[2] = {d->D, value_dim(d)};
+  const char* dnames[2] = {"D", "Dv"};
+  for (int i = 0; i < 2; ++i) {
+    if (dims[i] > 128)
+      return fail(NXA_E_UNSUPPORTED, "head dim %s=%d exceeds 128", dnames[i], dims[i]);
+    if (dims[i] % epc != 0)
+      return fail(NXA_E_UNSUPPORTED, "head dim %s=%d must be a multiple of %d",
+                  dnames[i], dims[i], epc);
+  }
   const int64_t rows = (int64_t)d->B * d->H * (int64_t)(d->Lq > d->Lk ? d->Lq : d->Lk);
   if (rows >= (int64_t)1 << 31)
     return fail(NXA_E_SHAPE, "B*H*L = %lld exceeds 2^31", (long long)rows);
@@ -259,6 +273,7 @@ nxa::Params base_params(const nxa_desc* d, const void* q, const void* k,
   p.Lq = d->Lq;
   p.Lk = d->Lk;
   p.D = d->D;
+  p.Dv = value_dim(d);
   p.scale = d->scale;
   p.scale_log2 = d->scale * nxa::kLog2e;
   p.causal = d->causal ? 1 : 0;
@@ -352,7 +367,7 @@ int nxa_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
                        stream);
     if (rc) return rc;
   }
-  const int dp = d->D <= 64 ? 64 : 128;
+  const int dp = padded_dim(d);
   return launch("fwd", stream, [&] { nxa::launch_fwd(p, d->io_dtype, dp, stream); });
 }
 
@@ -420,7 +435,7 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
       for (int i = 0; i < 3; ++i) p.dbias_str[i] = dbias_str[i];
     }
   }
-  const int dp = d->D <= 64 ? 64 : 128;
+  const int dp = padded_dim(d);
   if (io16 &&
       (rc = launch("dq", stream, [&] { nxa::launch_dq(p, d->io_dtype, dp, stream); })))
     return rc;

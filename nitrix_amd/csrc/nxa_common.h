@@ -79,6 +79,7 @@ struct Params {
   int64_t tm_str[3];                                 // tile-map B, H, Q-tile
 
   int B, H, Lq, Lk, D;
+  int Dv;              // head dim of v, o, dO, dv (D: q, k, dq, dk)
   int nqt;             // query tiles of the launching kernel (grid decode)
   int nkt;             // key tiles of the launching kernel
   float scale;

@@ -178,9 +178,9 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const Params p) {
       const int idx = tid + i * 256;
       const int r = idx / CPR, d = (idx % CPR) * EPC;
       const int key = k0 + r;
-      const bool ok = key < p.Lk && d < p.D;
-      kst[i] = ok ? ld16(kp + (int64_t)key * ks + d) : zero_frag<T>();
-      vst[i] = ok ? ld16(vp + (int64_t)key * vs + d) : zero_frag<T>();
+      const bool ok = key < p.Lk;
+      kst[i] = ok && d < p.D ? ld16(kp + (int64_t)key * ks + d) : zero_frag<T>();
+      vst[i] = ok && d < p.Dv ? ld16(vp + (int64_t)key * vs + d) : zero_frag<T>();
     }
   };
   auto lstore = [&](int buf) {
@@ -329,7 +329,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const Params p) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int d0 = db * 32 + 8 * c + 4 * g;
-        if (d0 < p.D) store4(op + d0, oacc[db], 4 * c, inv);
+        if (d0 < p.Dv) store4(op + d0, oacc[db], 4 * c, inv);
       }
     if (g == 0 && p.lse)
       p.lse[((int64_t)b * p.H + h) * p.Lq + qrow] =

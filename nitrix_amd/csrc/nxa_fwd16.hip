@@ -243,7 +243,7 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd16_kernel(const Params p) {
   // --- copies ------------------------------------------------------------------
   KS ksm, vsm;
   ksm.init(ks, p.D, wave, lane);
-  vsm.init(vs, p.D, wave, lane);
+  vsm.init(vs, p.Dv, wave, lane);
   const uint32_t lds0 = lds_offset(ring);
   const uint32_t ldsb = lds_offset(bring);
 
@@ -276,7 +276,7 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd16_kernel(const Params p) {
     const int k0 = tile_of(i) * BN;
     const uint32_t at = lds0 + (i % NST) * STAGE_BYTES;
     ksm.issue(kp, ks, k0, p.Lk, p.D, at, wave, lane);
-    vsm.issue(vp, vs, k0, p.Lk, p.D, at + TILE_BYTES, wave, lane);
+    vsm.issue(vp, vs, k0, p.Lk, p.Dv, at + TILE_BYTES, wave, lane);
     if constexpr (BMODE == kFbRow) {
       const int kk = min(k0 + 2 * c32, p.Lk - 2);
       dma4_sv(bp, 2u * (uint32_t)kk, at + 2 * TILE_BYTES + wave * 256);
@@ -647,7 +647,7 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd16_kernel(const Params p) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int d0 = db * 32 + 8 * c + 4 * g;
-        if (d0 < p.D) store4(op + d0, oacc[db], 4 * c, inv);
+        if (d0 < p.Dv) store4(op + d0, oacc[db], 4 * c, inv);
       }
     if (g == 0 && p.lse)
       p.lse[((int64_t)b * p.H + h) * p.Lq + qrow] = (m_ref + __log2f(l)) * kLn2;

@@ -44,7 +44,7 @@ def test_header_declares_the_expected_api():
 def test_library_exports_every_declared_function(lib):
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.nxa_version() == 1
+    assert lib.nxa_version() == 2
 
 
 def _desc(B=2, H=3, Lq=100, Lk=70, D=64, dtype=_lib.NXA_BF16):
@@ -70,6 +70,9 @@ def test_valid_descriptor(lib):
     assert _check(lib, _desc()) == _lib.NXA_OK
     assert _check(lib, _desc(dtype=_lib.NXA_F32, D=12)) == _lib.NXA_OK
     assert _check(lib, _desc(dtype=_lib.NXA_F16, D=40)) == _lib.NXA_OK
+    d = _desc(D=64)
+    d.Dv = 128  # value head dim different from the query / key one
+    assert _check(lib, d) == _lib.NXA_OK
 
 
 def test_fp16_head_dim_multiple_of_8(lib):
@@ -92,6 +95,9 @@ def test_mixed_bias_dtype_is_valid(lib):
         (lambda d: setattr(d, 'Lq', 0), _lib.NXA_E_SHAPE, 'positive'),
         (lambda d: setattr(d, 'D', 136), _lib.NXA_E_UNSUPPORTED, 'exceeds 128'),
         (lambda d: setattr(d, 'D', 12), _lib.NXA_E_UNSUPPORTED, 'multiple of 8'),
+        (lambda d: setattr(d, 'Dv', 136), _lib.NXA_E_UNSUPPORTED, 'Dv=136 exceeds 128'),
+        (lambda d: setattr(d, 'Dv', 20), _lib.NXA_E_UNSUPPORTED, 'Dv=20 must be a multiple'),
+        (lambda d: setattr(d, 'Dv', -8), _lib.NXA_E_SHAPE, 'negative'),
         (lambda d: d.q_str.__setitem__(2, 65), _lib.NXA_E_LAYOUT, 'stride'),
         (lambda d: d.k_str.__setitem__(0, -64), _lib.NXA_E_LAYOUT, 'negative'),
         (lambda d: d.bias_str.__setitem__(1, -1), _lib.NXA_E_LAYOUT, 'bias'),

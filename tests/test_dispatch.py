@@ -145,7 +145,10 @@ def test_validate_raises_value_error(shapes):
         (torch.float16, 24, 24, True),
         (torch.float16, 12, 12, False),
         (torch.float64, 64, 64, False),
-        (torch.bfloat16, 64, 32, False),
+        (torch.bfloat16, 64, 32, True),
+        (torch.float32, 64, 12, True),
+        (torch.bfloat16, 64, 136, False),
+        (torch.bfloat16, 64, 20, False),
         (torch.bfloat16, 136, 136, False),
         (torch.bfloat16, 12, 12, False),
     ],

@@ -78,15 +78,16 @@ def _make_mask(rng, kind, B, H, s, t):
 
 
 def _check(dtype, B, H, s, t, d, *, bias_shape=None, bias_dtype=None,
-           mask_kind=None, causal=False, seed=0, grads=True, scale=None):
+           mask_kind=None, causal=False, seed=0, grads=True, scale=None, dv=None):
     rng = np.random.default_rng(seed)
+    dv = d if dv is None else dv
     q = _draw(rng, (B, H, s, d), dtype)
     k = _draw(rng, (B, H, t, d), dtype)
-    v = _draw(rng, (B, H, t, d), dtype)
+    v = _draw(rng, (B, H, t, dv), dtype)
     bdt = bias_dtype or dtype
     bias = None if bias_shape is None else _draw(rng, bias_shape, bdt)
     mask = _make_mask(rng, mask_kind, B, H, s, t)
-    g = _draw(rng, (B, H, s, d), dtype)
+    g = _draw(rng, (B, H, s, dv), dtype)
     explicit_scale = scale
     if scale is None:
         scale = 1.0 / np.sqrt(d)
@@ -96,7 +97,7 @@ def _check(dtype, B, H, s, t, d, *, bias_shape=None, bias_dtype=None,
     tm = None if mask is None else torch.from_numpy(mask).to(_dev())
     from nitrix_amd import scaled_dot_product_attention
 
-    print(f'[case] {dtype} B{B} H{H} s{s} t{t} d{d} bias={bias_shape} '
+    print(f'[case] {dtype} B{B} H{H} s{s} t{t} d{d} dv{dv} bias={bias_shape} '
           f'mask={mask_kind} causal={causal} seed={seed}', flush=True)
     out = scaled_dot_product_attention(
         tq, tk, tv, bias=tb, mask=tm, causal=causal, scale=explicit_scale,
@@ -147,6 +148,20 @@ def test_dense(dtype, d):
                                    (130, 129, 40), (1, 65, 64)])
 def test_tails_and_padded_head_dim(dtype, s, t, d):
     _check(dtype, 2, 3, s, t, d, seed=s + t)
+
+
+@pytest.mark.parametrize('dtype', DTYPES, ids=IDS)
+@pytest.mark.parametrize('d,dv,kw', [
+    (64, 128, {}),
+    (128, 64, {'causal': True}),
+    (40, 24, {'bias_shape': (2, 2, 150, 170), 'mask_kind': 'random'}),
+    (64, 32, {'bias_shape': (1, 2, 1, 176), 'mask_kind': 'keypad'}),
+], ids=['64_128', '128_64_causal', '40_24_bias_mask', '64_32_rowbias'])
+def test_value_head_dim_differs(dtype, d, dv, kw):
+    """v / out / dO / dv with their own head dim d_v != d (the kernels pad
+    both to the same width; q.k runs over d, P.v over d_v)."""
+    t = 176 if kw.get('bias_shape', (0,))[-1] == 176 else 170
+    _check(dtype, 2, 2, 150, t, d, dv=dv, seed=30 + d + dv, **kw)
 
 
 @pytest.mark.parametrize('dtype', DTYPES, ids=IDS)

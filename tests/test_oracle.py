@@ -198,20 +198,20 @@ def test_causal_cross_is_top_left_aligned():
 # --- backward: central finite differences (float64) -------------------------
 
 
-def _fd_check(bias_shape, causal, with_mask, seed=21):
+def _fd_check(bias_shape, causal, with_mask, seed=21, dv=3):
     rng = np.random.RandomState(seed)
     b, h, s, t, d = 2, 2, 3, 4, 3
     if causal:
         t = s
     q = rng.standard_normal((b, h, s, d))
     k = rng.standard_normal((b, h, t, d))
-    v = rng.standard_normal((b, h, t, d))
+    v = rng.standard_normal((b, h, t, dv))
     bias = None if bias_shape is None else rng.standard_normal(bias_shape(s, t))
     mask = None
     if with_mask:
         mask = rng.rand(b, 1, s, t) > 0.3
         mask[..., 0] = True
-    g = rng.standard_normal((b, h, s, d))
+    g = rng.standard_normal((b, h, s, dv))
     scale = 0.7
 
     def loss(q, k, v, bias):
@@ -259,6 +259,12 @@ def test_backward_fd_query_broadcast_bias_causal():
 
 def test_backward_fd_no_bias_causal_masked():
     _fd_check(None, causal=True, with_mask=True)
+
+
+@pytest.mark.parametrize('dv', [2, 5])
+def test_backward_fd_value_head_dim_differs(dv):
+    # v, out, dO and dv carry their own head dim d_v != d.
+    _fd_check(lambda s, t: (2, 2, s, t), causal=True, with_mask=True, dv=dv)
 
 
 # --- bf16 semantics -----------------------------------------------------------
