@@ -84,7 +84,25 @@ CONFIGS = {
         workload='bf16 attention fwd+bwd, block-sparse mask [1,1,L,L] (128x128 blocks, '
         'p=0.25, diagonal kept), bias [1,8,1,L] (BASELINE configs[4])',
     ),
+    # Measurement lines of the widened path (not BASELINE configurations).
+    'c2f16': dict(
+        io='f16', B=8, H=16, L=4096, D=128, bias=None, mask='keypad', causal=False,
+        bwd=True,
+        workload='fp16 attention fwd+bwd, key-padding mask (C2 in fp16)',
+    ),
+    'w256': dict(
+        io='bf16', B=4, H=16, L=4096, D=256, bias=None, mask=None, causal=False,
+        bwd=True,
+        workload='bf16 attention fwd+bwd, head dim 256',
+    ),
+    'w256f32': dict(
+        io='f32', B=1, H=16, L=2048, D=256, bias=None, mask=None, causal=False,
+        bwd=True,
+        workload='fp32 attention fwd+bwd, head dim 256',
+    ),
 }
+
+_ROUND = {'bf16': 'round_bf16', 'f16': 'round_f16'}
 
 
 def _valid_lengths(B, L):
@@ -120,7 +138,7 @@ def _cpu_baseline(name, cfg, budget_s: float = 12.0):
     from oracle import attention as O
 
     B, H, L, D = cfg['B'], cfg['H'], cfg['L'], cfg['D']
-    bf = cfg['io'] == 'bf16'
+    rnd = getattr(O, _ROUND[cfg['io']]) if cfg['io'] in _ROUND else None
     rng = np.random.Generator(np.random.PCG64(SEED + 1))
     scale = 1.0 / math.sqrt(D)
     rows = min(L, 1024)
@@ -130,7 +148,7 @@ def _cpu_baseline(name, cfg, budget_s: float = 12.0):
 
     def draw(shape):
         x = rng.standard_normal(shape, dtype=np.float32)
-        return O.round_bf16(x) if bf else x
+        return rnd(x) if rnd else x
 
     def sample(n):
         b = n % B
@@ -193,7 +211,7 @@ class Workload:
     def __init__(self, name, cfg, torch, dev):
         self.name, self.cfg = name, cfg
         B, H, L, D = cfg['B'], cfg['H'], cfg['L'], cfg['D']
-        dtype = torch.bfloat16 if cfg['io'] == 'bf16' else torch.float32
+        dtype = {'bf16': torch.bfloat16, 'f16': torch.float16}.get(cfg['io'], torch.float32)
         self.dtype = dtype
         gen = torch.Generator(device=dev)
         gen.manual_seed(SEED)
@@ -246,7 +264,7 @@ class Workload:
         self.desc = desc
         self.fwd_flops = 4.0 * D * kept
         self.step_flops = (14.0 if bwd else 4.0) * D * kept
-        el = 2 if dtype == torch.bfloat16 else 4
+        el = torch.empty((), dtype=dtype).element_size()
         qkvo = 4 * B * H * L * D * el
         self.fwd_bytes = qkvo + B * H * L * 4 + (
             self.bias.numel() * self.bias.element_size() if self.bias is not None else 0
@@ -356,7 +374,7 @@ def main() -> int:
             kernels[kname] = {'avg_ms': tot / n, 'launches_per_step': n / prof_steps}
     _lib.profile_reset()
 
-    peak = PEAK_BF16_TFLOPS if cfg['io'] == 'bf16' else PEAK_F32_TFLOPS
+    peak = PEAK_BF16_TFLOPS if cfg['io'] in ('bf16', 'f16') else PEAK_F32_TFLOPS
     per_pair = {'fwd': 4.0 * D, 'dkdv': 8.0 * D, 'dq': 6.0 * D}
     dom = max(
         (k_ for k_ in kernels if k_ in per_pair),

@@ -65,7 +65,7 @@ enum {
 };
 
 typedef struct {
-  int32_t B, H, Lq, Lk, D;  /* head dim of q, k; D <= 128, D % 8 == 0 (bf16,
+  int32_t B, H, Lq, Lk, D;  /* head dim of q, k; D <= 256, D % 8 == 0 (bf16,
                                fp16) or % 4 (fp32)                            */
   int32_t io_dtype;         /* nxa_dtype of q, k, v, o, dO, dq, dk, dv       */
   int32_t bias_dtype;       /* nxa_dtype of bias and dbias                   */

@@ -54,7 +54,7 @@ _IO_DTYPES = {
 }
 # Bias dtypes the kernels read natively (others are upcast to float32).
 _BIAS_DTYPES = _IO_DTYPES
-_MAX_HEAD_DIM = 128
+_MAX_HEAD_DIM = 256
 
 
 class HipNotTileable(RuntimeError):
@@ -160,7 +160,7 @@ def _check_tileable(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
     """Reject shapes the gfx950 kernels cannot run (``attention.py:708-765``).
 
     Accepts bf16, fp16 or fp32 (q, k, v of one dtype), head dims ``d`` (q, k)
-    and ``d_v`` (v) up to 128 each (multiples of 8 for the 16-bit types, of 4
+    and ``d_v`` (v) up to 256 each (multiples of 8 for the 16-bit types, of 4
     for fp32) and any positive query / key lengths (tails are predicated in
     the kernels).
     """

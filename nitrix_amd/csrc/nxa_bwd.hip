@@ -1,5 +1,6 @@
-// Backward pass: delta = rowsum(O * dO), the fp32 dK/dV and dQ kernels (the
-// 16-bit ones live in nxa_bwd16.hip), the dbias reduction and the launchers.
+// Backward pass: delta = rowsum(O * dO), the dK/dV and dQ kernels for fp32
+// I/O and for every I/O dtype at padded head dims above 128 (the 16-bit ones
+// up to 128 live in nxa_bwd16.hip), the dbias reduction and the launchers.
 // Two deterministic kernels
 // (no atomics): dK/dV (+ dbias) with a grid over key tiles, and dQ with a
 // grid over query tiles.  Both recompute P from the forward's LSE.
@@ -17,9 +18,9 @@ namespace nxa {
 // ---------------------------------------------------------------------------
 // ndelta[b, h, q] = -sum_d O[q, d] * dO[q, d]  (fp32) and nlse2 = -lse * log2(e),
 // so the backward kernels stream both per-row values straight from memory
-// (negated: the 16-bit kernels start their MFMA accumulators at them).  Only
-// fp32 I/O runs this pass; with 16-bit I/O the dQ kernel computes both for its
-// own rows.
+// (negated: the 16-bit kernels start their MFMA accumulators at them).  The
+// kernels of this file need it; with 16-bit I/O up to DP = 128 the dQ kernel
+// computes both for its own rows instead.
 // 16 lanes per row.
 // ---------------------------------------------------------------------------
 template <typename T>
@@ -78,7 +79,7 @@ __device__ __forceinline__ void load_tile(const T* src, int64_t rs, int r0,
       *reinterpret_cast<Frag*>(&dst[(r + 1) * SK + d]) = x1;
 #pragma unroll
       for (int j = 0; j < EPC; ++j) {
-        bf16 pair[2] = {x0[j], x1[j]};
+        T pair[2] = {x0[j], x1[j]};
         *reinterpret_cast<uint32_t*>(&dstT[(d + j) * STT + r]) =
             *reinterpret_cast<uint32_t*>(pair);
       }
@@ -105,21 +106,35 @@ __device__ __forceinline__ void store_dbias(const Params& p, int64_t off,
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV (and dbias).  Block = 4 waves x 32 keys; loops over 64-query tiles.
-// Each wave computes S = Q K^T and dP = dO V^T with the key as the lane's
-// column, so P and dS feed dV^T = dO^T P and dK^T = Q^T dS as reduction
-// operands straight from registers.
+// dK / dV (and dbias).  Block = 4 waves x 32 keys; loops over query tiles
+// (64 queries; 32 at DP = 256, to fit LDS).  Each wave computes S = Q K^T and
+// dP = dO V^T with the key as the lane's column, so P and dS feed
+// dV^T = dO^T P and dK^T = Q^T dS as reduction operands straight from
+// registers.  OUT selects the outputs (kOutDv, kOutDk = dK and dbias, or
+// both) and CW the head-dim columns accumulated (kColAll, or one half:
+// kColLo / kColHi).  At DP = 256 dV and dK take passes of their own (fp32
+// dK two, one per half), so that the stationary K and V and one set of
+// accumulators fit a wave's 512 registers; dbias comes with the first dK
+// pass.
 // ---------------------------------------------------------------------------
-template <typename T, int DP>
+enum : int { kOutDv = 1, kOutDk = 2, kOutBoth = 3 };
+enum : int { kColAll = 0, kColLo = 1, kColHi = 2 };
+
+template <typename T, int DP, int OUT, int CW = kColAll>
 __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
   using M = Mma<T>;
   using Frag = typename M::Frag;
   constexpr int EPC = M::EPC, KC = M::KC;
-  constexpr int BNK = 128, BQ = 64;
+  constexpr int BNK = 128, BQ = DP > 128 ? 32 : 64;
+  constexpr int NQB = BQ / 32;  // 32-query blocks per tile
+  constexpr bool DV = OUT & kOutDv, DK = OUT & kOutDk;
+  constexpr bool DBIAS = DK && CW != kColHi;  // dbias in this pass
   constexpr int SK = DP + EPC;
   constexpr int ST = BQ + 4;
   constexpr int NC = DP / KC;
   constexpr int NDB = DP / 32;
+  constexpr int NDW = CW == kColAll ? NDB : NDB / 2;  // 32-column blocks accumulated
+  constexpr int DB0 = CW == kColHi ? NDB / 2 : 0;     // the first of them
   constexpr int FPB = M::FRAGS_PER_BLOCK;
   __shared__ __attribute__((aligned(16))) T Qs[BQ * SK];
   __shared__ __attribute__((aligned(16))) T Qt[DP * ST];
@@ -146,20 +161,21 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
   const float* lsep = p.lse + ((int64_t)b * p.H + h) * p.Lq;
   const float* ndltp = p.ndelta + ((int64_t)b * p.H + h) * p.Lq;
 
-  Frag kf[NC], vf[NC];
+  Frag kf[NC], vf[DK ? NC : 1];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int d = c * KC + g * EPC;
     kf[c] = kok && d < p.D ? ld16(kp + (int64_t)key * p.k_str[2] + d) : zero_frag<T>();
-    vf[c] = kok && d < p.Dv ? ld16(vp + (int64_t)key * p.v_str[2] + d) : zero_frag<T>();
+    if constexpr (DK)
+      vf[c] = kok && d < p.Dv ? ld16(vp + (int64_t)key * p.v_str[2] + d) : zero_frag<T>();
   }
-  f32x16 dk[NDB], dv[NDB];
+  f32x16 dk[DK ? NDW : 1], dv[DV ? NDW : 1];
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
+  for (int w = 0; w < NDW; ++w)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      dk[db][r] = 0.f;
-      dv[db][r] = 0.f;
+      if constexpr (DK) dk[w][r] = 0.f;
+      if constexpr (DV) dv[w][r] = 0.f;
     }
   float colsum = 0.f;
 
@@ -169,7 +185,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
       p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] + kclamp
                  : nullptr;
   const int64_t dbbase = b * p.dbias_str[0] + h * p.dbias_str[1] + key;
-  const bool full_db = p.dbias_mode == kDbiasFull;
+  const bool full_db = DBIAS && p.dbias_mode == kDbiasFull;
 
   const int nq = (p.Lq + BQ - 1) / BQ;
   for (int qt = 0; qt < nq; ++qt) {
@@ -196,9 +212,9 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
     }
     __syncthreads();
 
-    f32x16 s[2], dp[2];
+    f32x16 s[NQB], dp[NQB];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         s[qb][r] = 0.f;
@@ -208,7 +224,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
       for (int c = 0; c < NC; ++c) {
         const int off = (qb * 32 + c32) * SK + c * KC + g * EPC;
         M::run(s[qb], ld16(&Qs[off]), kf[c]);
-        M::run(dp[qb], ld16(&Ds[off]), vf[c]);
+        if constexpr (DK) M::run(dp[qb], ld16(&Ds[off]), vf[c]);
       }
     }
 
@@ -216,7 +232,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
     const bool diag = p.causal && (kw0 + 31 > q0);
     const bool tail = (q0 + BQ > p.Lq) || (kw0 + 32 > p.Lk);
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int qb = 0; qb < NQB; ++qb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int ql = qb * 32 + 8 * (r / 4) + 4 * g + (r % 4);
@@ -238,19 +254,22 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
         dp[qb][r] = ds;
         if (full_db && kok && q < p.Lq)
           store_dbias(p, dbbase + (int64_t)q * p.dbias_str[2], ds);
-        colsum += ds;
+        if constexpr (DBIAS) colsum += ds;
       }
 
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
+    for (int w = 0; w < NDW; ++w) {
+      const int db = DB0 + w;
       const T* rowd = &Dt[(db * 32 + c32) * ST];
       const T* rowq = &Qt[(db * 32 + c32) * ST];
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+      for (int qb = 0; qb < NQB; ++qb)
 #pragma unroll
         for (int f = 0; f < FPB; ++f) {
-          M::run(dv[db], lds_frag_t<T>(rowd + qb * 32, g, f), M::pack(s[qb], f));
-          M::run(dk[db], lds_frag_t<T>(rowq + qb * 32, g, f), M::pack(dp[qb], f));
+          if constexpr (DV)
+            M::run(dv[w], lds_frag_t<T>(rowd + qb * 32, g, f), M::pack(s[qb], f));
+          if constexpr (DK)
+            M::run(dk[w], lds_frag_t<T>(rowq + qb * 32, g, f), M::pack(dp[qb], f));
         }
     }
   }
@@ -259,18 +278,20 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
     T* dkp = (T*)p.dk + b * p.k_str[0] + h * p.k_str[1] + (int64_t)key * p.k_str[2];
     T* dvp = (T*)p.dv + b * p.v_str[0] + h * p.v_str[1] + (int64_t)key * p.v_str[2];
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+    for (int w = 0; w < NDW; ++w)
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const int d0 = db * 32 + 8 * c + 4 * g;
+        const int d0 = (DB0 + w) * 32 + 8 * c + 4 * g;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          if (d0 < p.D) dkp[d0 + j] = from_f32<T>(dk[db][4 * c + j] * p.scale);
-          if (d0 < p.Dv) dvp[d0 + j] = from_f32<T>(dv[db][4 * c + j]);
+          if constexpr (DK)
+            if (d0 < p.D) dkp[d0 + j] = from_f32<T>(dk[w][4 * c + j] * p.scale);
+          if constexpr (DV)
+            if (d0 < p.Dv) dvp[d0 + j] = from_f32<T>(dv[w][4 * c + j]);
         }
       }
   }
-  if (p.dbias_mode == kDbiasColsum) {
+  if (DBIAS && p.dbias_mode == kDbiasColsum) {
     const float tot = colsum + shfl_xor32(colsum);
     if (kok && g == 0) store_dbias(p, dbbase, tot);
   }
@@ -281,16 +302,21 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
 // computes S^T = K Q^T and dP^T = V dO^T (query = lane column) so dS^T feeds
 // dQ^T = K^T dS^T from registers.
 // ---------------------------------------------------------------------------
-template <typename T, int DP>
+// CW as in dkdv_kernel: at DP = 256 fp32 dQ takes two passes, one per half of
+// its columns (the stationary Q and dO fill half of a wave's registers).
+template <typename T, int DP, int CW = kColAll>
 __global__ __launch_bounds__(256) void dq_kernel(const Params p) {
   using M = Mma<T>;
   using Frag = typename M::Frag;
   constexpr int EPC = M::EPC, KC = M::KC;
-  constexpr int BM = 128, BN = 64;
+  constexpr int BM = 128, BN = DP > 128 ? 32 : 64;
+  constexpr int NKB = BN / 32;  // 32-key blocks per tile
   constexpr int SK = DP + EPC;
   constexpr int ST = BN + 4;
   constexpr int NC = DP / KC;
   constexpr int NDB = DP / 32;
+  constexpr int NDW = CW == kColAll ? NDB : NDB / 2;
+  constexpr int DB0 = CW == kColHi ? NDB / 2 : 0;
   constexpr int FPB = M::FRAGS_PER_BLOCK;
   __shared__ __attribute__((aligned(16))) T Ks[BN * SK];
   __shared__ __attribute__((aligned(16))) T Vs[BN * SK];
@@ -324,11 +350,11 @@ __global__ __launch_bounds__(256) void dq_kernel(const Params p) {
   const float lse2 = p.lse[rowid] * kLog2e;
   const float dlt = -p.ndelta[rowid];
 
-  f32x16 dq[NDB];
+  f32x16 dq[NDW];
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
+  for (int w = 0; w < NDW; ++w)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
+    for (int r = 0; r < 16; ++r) dq[w][r] = 0.f;
 
   int k_end = p.Lk;
   if (p.causal) k_end = min(k_end, q0 + BM);
@@ -352,9 +378,9 @@ __global__ __launch_bounds__(256) void dq_kernel(const Params p) {
     load_tile<T, DP, BN, SK, ST, false>(vp, p.v_str[2], k0, p.Lk, p.Dv, Vs, nullptr, tid);
     __syncthreads();
 
-    f32x16 s[2], dp[2];
+    f32x16 s[NKB], dp[NKB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         s[kb][r] = 0.f;
@@ -372,7 +398,7 @@ __global__ __launch_bounds__(256) void dq_kernel(const Params p) {
     const bool diag = p.causal && (k0 + BN - 1 > qw0);
     const bool tail = k0 + BN > p.Lk;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int key0 = k0 + kb * 32 + 8 * c + 4 * g;
@@ -394,27 +420,27 @@ __global__ __launch_bounds__(256) void dq_kernel(const Params p) {
       }
 
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const T* row = &Kt[(db * 32 + c32) * ST];
+    for (int w = 0; w < NDW; ++w) {
+      const T* row = &Kt[((DB0 + w) * 32 + c32) * ST];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int f = 0; f < FPB; ++f)
-          M::run(dq[db], lds_frag_t<T>(row + kb * 32, g, f), M::pack(dp[kb], f));
+          M::run(dq[w], lds_frag_t<T>(row + kb * 32, g, f), M::pack(dp[kb], f));
     }
   }
 
   if (qok) {
     T* dqp = (T*)p.dq + b * p.q_str[0] + h * p.q_str[1] + (int64_t)qrow * p.q_str[2];
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+    for (int w = 0; w < NDW; ++w)
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const int d0 = db * 32 + 8 * c + 4 * g;
+        const int d0 = (DB0 + w) * 32 + 8 * c + 4 * g;
         if (d0 < p.D) {
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            dqp[d0 + j] = from_f32<T>(dq[db][4 * c + j] * p.scale);
+            dqp[d0 + j] = from_f32<T>(dq[w][4 * c + j] * p.scale);
         }
       }
   }
@@ -452,35 +478,65 @@ __global__ __launch_bounds__(256) void dbias_reduce_kernel(
 void launch_delta(const Params& p, int io_dtype, hipStream_t stream) {
   const int rows = p.B * p.H * p.Lq;
   const int n = (rows + 15) / 16;
-  (void)io_dtype;  // fp32 only (see delta_kernel)
-  hipLaunchKernelGGL(delta_kernel<float>, dim3(n), dim3(256), 0, stream, p);
+  if (io_dtype == kBF16)
+    hipLaunchKernelGGL(delta_kernel<bf16>, dim3(n), dim3(256), 0, stream, p);
+  else if (io_dtype == kF16)
+    hipLaunchKernelGGL(delta_kernel<f16>, dim3(n), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(delta_kernel<float>, dim3(n), dim3(256), 0, stream, p);
 }
 
-template <typename T, int DP>
+template <typename T, int DP, int OUT, int CW = kColAll>
 static void launch_dkdv_t(Params p, hipStream_t stream) {
   p.nkt = (p.Lk + 127) / 128;
   const int n = p.B * p.H * p.nkt;
-  hipLaunchKernelGGL((dkdv_kernel<T, DP>), dim3(n), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((dkdv_kernel<T, DP, OUT, CW>), dim3(n), dim3(256), 0, stream, p);
 }
 
 void launch_dkdv(const Params& p, int io_dtype, int dp, hipStream_t stream) {
-  if (io_dtype == kBF16 || io_dtype == kF16) {
+  if (dp == 256) {
+    if (io_dtype == kBF16) {
+      launch_dkdv_t<bf16, 256, kOutDv>(p, stream);
+      launch_dkdv_t<bf16, 256, kOutDk>(p, stream);
+    } else if (io_dtype == kF16) {
+      launch_dkdv_t<f16, 256, kOutDv>(p, stream);
+      launch_dkdv_t<f16, 256, kOutDk>(p, stream);
+    } else {
+      launch_dkdv_t<float, 256, kOutDv>(p, stream);
+      launch_dkdv_t<float, 256, kOutDk, kColLo>(p, stream);
+      launch_dkdv_t<float, 256, kOutDk, kColHi>(p, stream);
+    }
+  } else if (io_dtype == kBF16 || io_dtype == kF16) {
     launch_dkdv16(p, io_dtype, dp, stream);
   } else {
-    if (dp == 64) launch_dkdv_t<float, 64>(p, stream);
-    else launch_dkdv_t<float, 128>(p, stream);
+    if (dp == 64) launch_dkdv_t<float, 64, kOutBoth>(p, stream);
+    else launch_dkdv_t<float, 128, kOutBoth>(p, stream);
   }
 }
 
-template <typename T, int DP>
+template <typename T, int DP, int CW = kColAll>
 static void launch_dq_t(Params p, hipStream_t stream) {
   p.nqt = (p.Lq + 127) / 128;
   const int n = p.B * p.H * p.nqt;
-  hipLaunchKernelGGL((dq_kernel<T, DP>), dim3(n), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((dq_kernel<T, DP, CW>), dim3(n), dim3(256), 0, stream, p);
+}
+
+template <typename T>
+static void launch_dq_wide(const Params& p, hipStream_t stream) {
+  if constexpr (sizeof(T) == 2) {
+    launch_dq_t<T, 256>(p, stream);
+  } else {
+    launch_dq_t<T, 256, kColLo>(p, stream);
+    launch_dq_t<T, 256, kColHi>(p, stream);
+  }
 }
 
 void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream) {
-  if (io_dtype == kBF16 || io_dtype == kF16) {
+  if (dp == 256) {
+    if (io_dtype == kBF16) launch_dq_wide<bf16>(p, stream);
+    else if (io_dtype == kF16) launch_dq_wide<f16>(p, stream);
+    else launch_dq_wide<float>(p, stream);
+  } else if (io_dtype == kBF16 || io_dtype == kF16) {
     launch_dq16(p, io_dtype, dp, stream);
   } else {
     if (dp == 64) launch_dq_t<float, 64>(p, stream);

@@ -37,10 +37,13 @@ bool known_dtype(int dt) { return dt == NXA_BF16 || dt == NXA_F32 || dt == NXA_F
 // Head dim of v / o (Dv = 0 means Dv = D).
 int value_dim(const nxa_desc* d) { return d->Dv > 0 ? d->Dv : d->D; }
 
+// Largest head dim (D or Dv) the kernels take.
+constexpr int kMaxHeadDim = 256;
+
 // Padded head-dim width the kernels are instantiated for.
 int padded_dim(const nxa_desc* d) {
   const int m = d->D > value_dim(d) ? d->D : value_dim(d);
-  return m <= 64 ? 64 : 128;
+  return m <= 64 ? 64 : m <= 128 ? 128 : 256;
 }
 
 // ---------------------------------------------------------------------------
@@ -99,8 +102,9 @@ int check_desc(const nxa_desc* d, int has_bias, int has_mask) {
   const int dims[2] = {d->D, value_dim(d)};
   const char* dnames[2] = {"D", "Dv"};
   for (int i = 0; i < 2; ++i) {
-    if (dims[i] > 128)
-      return fail(NXA_E_UNSUPPORTED, "head dim %s=%d exceeds 128", dnames[i], dims[i]);
+    if (dims[i] > kMaxHeadDim)
+      return fail(NXA_E_UNSUPPORTED, "head dim %s=%d exceeds %d", dnames[i], dims[i],
+                  kMaxHeadDim);
     if (dims[i] % epc != 0)
       return fail(NXA_E_UNSUPPORTED, "head dim %s=%d must be a multiple of %d",
                   dnames[i], dims[i], epc);
@@ -410,10 +414,11 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
   p.ndelta = reinterpret_cast<float*>(wsb + ws.delta);
   p.nlse2 = reinterpret_cast<float*>(
       wsb + ws.delta + align256((size_t)d->B * d->H * d->Lq * sizeof(float)));
-  // 16-bit I/O: the dQ kernel computes -delta and -lse * log2(e) for its own
-  // rows and runs first; fp32 has a pass of its own.
-  const bool io16 = d->io_dtype != NXA_F32;
-  if (!io16 && (rc = launch("delta", stream,
+  // 16-bit I/O up to a padded head dim of 128: the dQ kernel computes -delta
+  // and -lse * log2(e) for its own rows and runs first; the other kernels
+  // (fp32, and head dims above 128) have a pass of its own.
+  const bool dq_first = d->io_dtype != NXA_F32 && padded_dim(d) <= 128;
+  if (!dq_first && (rc = launch("delta", stream,
                                [&] { nxa::launch_delta(p, d->io_dtype, stream); })))
     return rc;
   if (mask) {
@@ -436,13 +441,13 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
     }
   }
   const int dp = padded_dim(d);
-  if (io16 &&
+  if (dq_first &&
       (rc = launch("dq", stream, [&] { nxa::launch_dq(p, d->io_dtype, dp, stream); })))
     return rc;
   if ((rc = launch("dkdv", stream,
                    [&] { nxa::launch_dkdv(p, d->io_dtype, dp, stream); })))
     return rc;
-  if (!io16 &&
+  if (!dq_first &&
       (rc = launch("dq", stream, [&] { nxa::launch_dq(p, d->io_dtype, dp, stream); })))
     return rc;
   if (dbias && dg.reduce) {

@@ -198,30 +198,26 @@ __device__ __forceinline__ typename Mma<T>::Frag zero_frag() {
 // row[8c + 4g].
 template <typename T>
 __device__ __forceinline__ typename Mma<T>::Frag lds_frag_t(const T* row,
-                                                            int g, int f);
-
-template <>
-__device__ __forceinline__ bf16x8 lds_frag_t<bf16>(const bf16* row, int g,
-                                                   int f) {
-  const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + 16 * f + 4 * g);
-  const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 16 * f + 8 + 4 * g);
-  bf16x8 r;
+                                                            int g, int f) {
+  using Frag = typename Mma<T>::Frag;
+  if constexpr (sizeof(T) == 4) {
+    return *reinterpret_cast<const Frag*>(row + 8 * f + 4 * g);
+  } else {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    const t4 lo = *reinterpret_cast<const t4*>(row + 16 * f + 4 * g);
+    const t4 hi = *reinterpret_cast<const t4*>(row + 16 * f + 8 + 4 * g);
+    Frag r;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    r[j] = lo[j];
-    r[4 + j] = hi[j];
+    for (int j = 0; j < 4; ++j) {
+      r[j] = lo[j];
+      r[4 + j] = hi[j];
+    }
+    return r;
   }
-  return r;
-}
-
-template <>
-__device__ __forceinline__ f32x4 lds_frag_t<float>(const float* row, int g,
-                                                   int f) {
-  return *reinterpret_cast<const f32x4*>(row + 8 * f + 4 * g);
 }
 
 // Reduction-operand fragment f of a 32x16 MFMA operand read *transposed*
-// from a row-major bf16 LDS tile whose rows are the reduction index:
+// from a row-major 16-bit LDS tile whose rows are the reduction index:
 // lane L receives tile[r0 + key(f, L/32, j)][col0 + L%32] for j = 0..7 with
 // key(f, g, j) = 16f + 8(j/4) + 4g + j%4 -- the row groups the accumulator
 // layout assigns to fragment f.
@@ -231,20 +227,22 @@ __device__ __forceinline__ f32x4 lds_frag_t<float>(const float* row, int g,
 // lane i of a group addresses row (r0 + 16f + 4g + i/4 [+8]) at column
 // (col0 + 16*(group%2) + 4*(i%4)).
 typedef short i16x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ bf16x8 lds_tr_frag(const bf16* tile, int stride,
-                                              int r0, int col0, int lane,
-                                              int f) {
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::Frag lds_tr_frag(const T* tile, int stride,
+                                                             int r0, int col0, int lane,
+                                                             int f) {
+  static_assert(sizeof(T) == 2, "16-bit tiles");
   const int grp = lane >> 4, i = lane & 15;
   const int row = r0 + 16 * f + 4 * (grp >> 1) + (i >> 2);
   const int col = col0 + 16 * (grp & 1) + 4 * (i & 3);
-  const bf16* p0 = tile + row * stride + col;
+  const T* p0 = tile + row * stride + col;
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
   const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
   const i16x4 hi =
       __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0 + 8 * stride));
   typedef short i16x8 __attribute__((ext_vector_type(8)));
   const i16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(bf16x8, r);
+  return __builtin_bit_cast(typename Mma<T>::Frag, r);
 }
 
 // XOR-swizzled bf16 tiles with DP columns and no row padding.  The 16-byte
@@ -267,73 +265,6 @@ __device__ __forceinline__ int swz_off(int row, int chunk) {
   return row * DP + 8 * (chunk ^ swz<DP>(row));
 }
 
-// lds_tr_frag for a swizzled tile (see lds_tr_frag for the lane mapping).
-template <int DP>
-__device__ __forceinline__ bf16x8 lds_tr_frag_swz(const bf16* tile, int r0,
-                                                  int col0, int lane, int f) {
-  const int grp = lane >> 4, i = lane & 15;
-  const int row = r0 + 16 * f + 4 * (grp >> 1) + (i >> 2);
-  const int col = col0 + 16 * (grp & 1) + 4 * (i & 3);
-  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-  const bf16* p0 = tile + swz_off<DP>(row, col >> 3) + (col & 7);
-  const bf16* p1 = tile + swz_off<DP>(row + 8, col >> 3) + (col & 7);
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
-  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p1);
-  typedef short i16x8 __attribute__((ext_vector_type(8)));
-  const i16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(bf16x8, r);
-}
-
-// ---------------------------------------------------------------------------
-// Row-permuted, padded bf16 tiles ("P-tiles").  Logical row r lives at
-// physical row tperm(r) (a 4x4 transpose inside every group of 16 rows), rows
-// are DP + 8 elements apart (16-byte pad).  With this layout
-//   * 16-byte row reads of 16 consecutive rows hit 16 distinct 16-byte bank
-//     groups (the pad alone spreads them);
-//   * ds_read_b64_tr_b16 reads, whose 32 lanes cover 4 consecutive rows x 64
-//     bytes, see those 4 rows 64 bytes apart (the permutation);
-// and both kinds of address are one per-lane base plus compile-time
-// immediates.  Tiles are filled by 1 KB direct copies: a 64-row tile is
-// exactly 64 * (DP / 8 + 1) 16-byte slots, the pad slots receive filler.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ int tperm(int r) {
-  return (r & ~15) | ((r & 3) << 2) | ((r >> 2) & 3);
-}
-
-template <int DP>
-struct PTile {
-  static constexpr int STRIDE = DP + 8;     // elements per physical row
-  static constexpr int SPR = DP / 8 + 1;    // 16-byte slots per row
-  static constexpr int ROWS = 64;
-  static constexpr int NI = ROWS * SPR / 64;  // 1 KB copies per tile
-  static constexpr int ELEMS = ROWS * STRIDE;
-  static_assert(ROWS * SPR % 64 == 0, "tile must be whole 1 KB copies");
-
-  // Element offset of the 16-byte row read (logical row, head-dim element d).
-  static __device__ __forceinline__ int row_off(int row, int d) {
-    return tperm(row) * STRIDE + d;
-  }
-};
-
-// Transposed MFMA operand fragment f from a P-tile (see lds_tr_frag for the
-// lane mapping): rows r0 + key(f, g, j), columns col0 + lane % 32.
-template <int DP>
-__device__ __forceinline__ bf16x8 ptile_tr_frag(const bf16* tile, int r0,
-                                                int col0, int lane, int f) {
-  constexpr int S = PTile<DP>::STRIDE;
-  const int grp = lane >> 4, i = lane & 15;
-  const int row = r0 + 16 * f + 4 * (grp >> 1) + (i >> 2);
-  const int col = col0 + 16 * (grp & 1) + 4 * (i & 3);
-  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-  const bf16* p0 = tile + tperm(row) * S + col;
-  const bf16* p1 = tile + tperm(row + 8) * S + col;
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p0);
-  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p1);
-  typedef short i16x8 __attribute__((ext_vector_type(8)));
-  const i16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(bf16x8, r);
-}
-
 // ---------------------------------------------------------------------------
 // Direct global -> LDS copies (no staging registers).  For one wave, lane l's
 // `size` bytes land at lds + l * size; the LDS address must be wave-uniform.
@@ -349,17 +280,6 @@ __device__ __forceinline__ bf16x8 ptile_tr_frag(const bf16* tile, int r0,
 __device__ __forceinline__ uint32_t lds_offset(const void* lds) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
 }
-__device__ __forceinline__ void dma16(const void* g, void* lds) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_offset(lds));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(g), "s"(m) : "m0");
-}
-__device__ __forceinline__ void dma4(const void* g, void* lds) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_offset(lds));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-               :: "v"(g), "s"(m) : "m0");
-}
-
 // Instruction classes of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedDsRead = 0x100,
               kSchedDsWrite = 0x200;
@@ -386,13 +306,6 @@ __device__ __forceinline__ void barrier_nofence() {
   asm volatile("" ::: "memory");
 }
 
-// Direct copy of 16 bytes per lane to LDS byte offset `lds` (wave-uniform).
-__device__ __forceinline__ void dma16_at(const void* g, uint32_t lds) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(g), "s"(m) : "m0");
-}
-
 // Direct copies addressed as a wave-uniform base (SGPR pair) plus a per-lane
 // 32-bit byte offset (the global_load "saddr" form): no 64-bit per-lane
 // address arithmetic and no 64-bit per-lane address registers.
@@ -406,59 +319,6 @@ __device__ __forceinline__ void dma4_sv(const void* base, uint32_t voff, uint32_
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
                :: "v"(voff), "s"(base), "s"(m) : "m0");
 }
-
-// Streams 64-row P-tiles of one [nrows, D] bf16 matrix (row stride rs
-// elements) into LDS.  Copy j of a tile is issued by wave (j + rot) % NW; the
-// lane's source offset inside the tile (row * rs + column) is computed once,
-// so a tile costs one 64-bit add per copy.  Rows past nrows are clamped to
-// the last row (only in the tail tile) and head-dim chunks past D (and pad
-// slots) read chunk 0 of the row: finite filler that callers mask or multiply
-// by zero.
-template <int DP, int NW>
-struct PTileStream {
-  static constexpr int NI = PTile<DP>::NI;
-  static constexpr int CNT = (NI + NW - 1) / NW;  // copies per wave (at most)
-  int64_t off[CNT];
-  int row[CNT];
-  int col[CNT];
-  int me;  // this wave's slot in the copy rotation
-
-  __device__ __forceinline__ void init(int64_t rs, int D, int wave, int rot,
-                                       int lane) {
-    constexpr int SPR = PTile<DP>::SPR;
-    me = (wave + NW - rot) % NW;
-#pragma unroll
-    for (int m = 0; m < CNT; ++m) {
-      const int s = (m * NW + me) * 64 + lane;
-      const int prow = s / SPR;
-      const int k = s - prow * SPR;
-      row[m] = tperm(prow);
-      col[m] = (k < SPR - 1 && k * 8 < D) ? k * 8 : 0;
-      off[m] = (int64_t)row[m] * rs + col[m];
-    }
-  }
-  // Number of copies this wave issues per tile.
-  __device__ __forceinline__ int count() const { return me < NI % NW ? CNT : NI / NW; }
-
-  // Copies rows r0.. of `src` into the tile at LDS byte offset `lds`.
-  __device__ __forceinline__ void issue(const bf16* src, int64_t rs, int r0,
-                                        int nrows, uint32_t lds) const {
-    if (r0 + 64 <= nrows) {
-      const bf16* base = src + (int64_t)r0 * rs;
-#pragma unroll
-      for (int m = 0; m < CNT; ++m)
-        if (m * NW + me < NI)  // wave-uniform
-          dma16_at(base + off[m], lds + (m * NW + me) * 1024);
-    } else {
-#pragma unroll
-      for (int m = 0; m < CNT; ++m)
-        if (m * NW + me < NI) {
-          const int r = min(r0 + row[m], nrows - 1);
-          dma16_at(src + (int64_t)r * rs + col[m], lds + (m * NW + me) * 1024);
-        }
-    }
-  }
-};
 
 // Streams 64-row XOR-swizzled [64 x DP] bf16 tiles (swz_off layout, no
 // padding) of one [nrows, D] matrix (row stride rs elements) into LDS with
@@ -544,45 +404,6 @@ __device__ __forceinline__ void dma4_buf(i32x4 rsrc, uint32_t voff, uint32_t lds
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
                :: "v"(voff), "s"(rsrc), "s"(m) : "m0");
 }
-
-// Direct copy of 4 bytes per lane to LDS byte offset `lds` (wave-uniform):
-// lane l's dword lands at lds + 4 l.
-__device__ __forceinline__ void dma4_at(const void* g, uint32_t lds) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-               :: "v"(g), "s"(m) : "m0");
-}
-
-// Fills a 64-row P-tile from rows r0.. of a [nrows, D] bf16 matrix (row stride
-// rs elements) with 1 KB direct copies; copy j is issued by wave j % NW.
-// Rows past nrows are clamped to the last row and head-dim chunks past D (and
-// pad slots) read chunk 0 of the row: finite filler that callers mask or
-// multiply by zero.
-template <int DP, int NW>
-struct PTileCopy {
-  static constexpr int NI = PTile<DP>::NI;
-  static constexpr int CNT_HI = (NI + NW - 1) / NW;  // copies of waves < N_HI
-  static constexpr int CNT_LO = NI / NW;             // copies of the others
-  static constexpr int N_HI = NI % NW;
-
-  static __device__ __forceinline__ void issue(const bf16* src, int64_t rs,
-                                               int r0, int nrows, int D,
-                                               bf16* tile, int wave, int lane) {
-    constexpr int SPR = PTile<DP>::SPR;
-#pragma unroll
-    for (int j0 = 0; j0 < NI; j0 += NW) {
-      const int j = j0 + wave;
-      if (j < NI) {  // wave-uniform
-        const int s = j * 64 + lane;
-        const int prow = s / SPR;
-        const int k = s - prow * SPR;
-        const int row = min(r0 + tperm(prow), nrows - 1);
-        const int col = (k < SPR - 1 && k * 8 < D) ? k * 8 : 0;
-        dma16(src + (int64_t)row * rs + col, tile + j * 512);
-      }
-    }
-  }
-};
 
 __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
 __device__ __forceinline__ float to_f32(f16 x) { return (float)x; }

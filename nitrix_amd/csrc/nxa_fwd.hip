@@ -75,16 +75,21 @@ __global__ __launch_bounds__(256) void tilemap_kernel(const Params p, int MB,
 }
 
 // ---------------------------------------------------------------------------
-// Forward kernel (fp32 I/O; 16-bit I/O has its own kernel with direct
-// global->LDS tile copies).  Block = 4 waves x 32 queries (128 rows); two blocks share
-// a CU, so one block's softmax (VALU, v_exp) overlaps the other's MFMAs.
-// 64-key K/V tiles stream through double-buffered LDS: the next tile is
-// fetched into registers while the current one is consumed.
+// Forward kernel for fp32 I/O, and for every I/O dtype at padded head dims
+// above 128 (16-bit I/O up to 128 has its own kernel with direct global->LDS
+// tile copies).  Block = 4 waves x 32 queries (128 rows).  Up to DP = 128 two
+// blocks share a CU, so one block's softmax (VALU, v_exp) overlaps the
+// other's MFMAs; at DP = 256 a block has the CU alone (one wave per SIMD,
+// up to 512 registers for the stationary Q and the O accumulators).  K/V
+// tiles (64 keys; 32 for fp32 at DP = 256, to fit LDS) stream through
+// double-buffered LDS: the next tile is fetched into registers while the
+// current one is consumed.
 //
 // Each wave computes S^T = K Q^T so that a lane owns one query row: the row
 // max / sum need one cross-lane exchange (lane l <-> l^32) and P feeds the
-// P.V product straight from registers as its reduction operand.  For bf16, V
-// stays row-major in LDS and is read transposed with ds_read_b64_tr_b16.
+// P.V product straight from registers as its reduction operand.  For 16-bit
+// I/O, V stays row-major in LDS and is read transposed with
+// ds_read_b64_tr_b16.
 //
 // The running max is only raised when a row's new maximum exceeds it by more
 // than kRescaleSlack (in log2 units): P is then bounded by 2^kRescaleSlack and
@@ -95,17 +100,18 @@ constexpr float kRescaleSlack = 8.0f;
 constexpr int kMaxTileClasses = 1024;  // per-block key-tile classes kept in LDS
 
 template <typename T, int DP, bool HAS_BIAS, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void fwd_kernel(const Params p) {
+__global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void fwd_kernel(const Params p) {
   using M = Mma<T>;
   using Frag = typename M::Frag;
-  constexpr bool kBF16 = sizeof(T) == 2;
+  constexpr bool k16 = sizeof(T) == 2;
   constexpr int EPC = M::EPC, KC = M::KC;
-  constexpr int BM = 128, BN = 64;
+  constexpr int BM = 128, BN = (DP > 128 && !k16) ? 32 : 64;
+  constexpr int NKB = BN / 32;                    // 32-key blocks per tile
   constexpr int SKK = DP + EPC;                   // K row stride (16 B pad)
-  constexpr int SKV = kBF16 ? DP + 32 : BN + 4;   // V row stride (bf16: row-major,
+  constexpr int SKV = k16 ? DP + 32 : BN + 4;     // V row stride (16-bit: row-major,
                                                   // 64 B pad; fp32: transposed)
   constexpr int KSZ = BN * SKK;
-  constexpr int VSZ = kBF16 ? BN * SKV : DP * SKV;
+  constexpr int VSZ = k16 ? BN * SKV : DP * SKV;
   constexpr int NC = DP / KC;
   constexpr int NDB = DP / 32;
   constexpr int CPR = DP / EPC;  // 16-byte chunks per row
@@ -191,7 +197,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const Params p) {
       const int idx = tid + i * 256;
       const int r = idx / CPR, d = (idx % CPR) * EPC;
       *reinterpret_cast<Frag*>(&Ks[r * SKK + d]) = kst[i];
-      if constexpr (kBF16) {
+      if constexpr (k16) {
         *reinterpret_cast<Frag*>(&Vs[r * SKV + d]) = vst[i];
       } else {
 #pragma unroll
@@ -213,22 +219,24 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const Params p) {
     const int cls = tclass(kt);
     int kn = kt + 1;
     while (kn < nkt && !(tclass(kn) & 1)) ++kn;
-    if (kn < nkt) gload(kn * BN);  // in flight while this tile is consumed
+    // In flight while this tile is consumed (at DP = 256 the staging
+    // registers are not free during the tile: the load follows it).
+    if (DP <= 128 && kn < nkt) gload(kn * BN);
 
     const T* Ks = smem + buf * (KSZ + VSZ);
     const T* Vs = Ks + KSZ;
     const int k0 = kt * BN;
 
-    // S^T = K Q^T: 64 keys (two 32-key blocks) x 32 queries.
-    f32x16 s[2];
+    // S^T = K Q^T: BN keys (NKB 32-key blocks) x 32 queries.
+    f32x16 s[NKB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
 #pragma unroll
     for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
         M::run(s[kb], ld16(&Ks[(kb * 32 + c32) * SKK + c * KC + g * EPC]),
                qf[c]);
 
@@ -242,7 +250,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const Params p) {
     if (general) {
       cc = 1.0f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int key0 = k0 + kb * 32 + 8 * c + 4 * g;
@@ -268,7 +276,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const Params p) {
     // Online softmax with a lazily raised reference max.
     float mt = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
     mt = fmaxf(mt, shfl_xor32(mt)) * cc;
@@ -285,7 +293,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const Params p) {
     const float neg_m = (m_ref == -INFINITY) ? 0.f : -m_ref;
     float rs = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float e = fast_exp2(__builtin_fmaf(s[kb][r], cc, neg_m));
@@ -296,14 +304,14 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const Params p) {
 
     // O^T += V^T P^T.
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int f = 0; f < FPB; ++f) {
         const Frag pf = M::pack(s[kb], f);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
           Frag a;
-          if constexpr (kBF16)
+          if constexpr (k16)
             a = lds_tr_frag(Vs, SKV, kb * 32, db * 32, lane, f);
           else
             a = lds_frag_t<T>(&Vs[(db * 32 + c32) * SKV + kb * 32], g, f);
@@ -311,6 +319,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const Params p) {
         }
       }
 
+    if (DP > 128 && kn < nkt) gload(kn * BN);
     if (kn < nkt) lstore(buf ^ 1);
     __syncthreads();
     buf ^= 1;
@@ -369,7 +378,11 @@ static void launch_fwd_flags(const Params& p, hipStream_t stream) {
 }
 
 void launch_fwd(const Params& p, int io_dtype, int dp, hipStream_t stream) {
-  if (io_dtype == kBF16 || io_dtype == kF16) {
+  if (dp == 256) {
+    if (io_dtype == kBF16) launch_fwd_flags<bf16, 256>(p, stream);
+    else if (io_dtype == kF16) launch_fwd_flags<f16, 256>(p, stream);
+    else launch_fwd_flags<float, 256>(p, stream);
+  } else if (io_dtype == kBF16 || io_dtype == kF16) {
     launch_fwd16(p, io_dtype, dp, stream);
   } else {
     if (dp == 64) launch_fwd_flags<float, 64>(p, stream);

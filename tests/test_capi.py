@@ -73,6 +73,8 @@ def test_valid_descriptor(lib):
     d = _desc(D=64)
     d.Dv = 128  # value head dim different from the query / key one
     assert _check(lib, d) == _lib.NXA_OK
+    assert _check(lib, _desc(D=256)) == _lib.NXA_OK
+    assert _check(lib, _desc(dtype=_lib.NXA_F32, D=196)) == _lib.NXA_OK
 
 
 def test_fp16_head_dim_multiple_of_8(lib):
@@ -93,9 +95,9 @@ def test_mixed_bias_dtype_is_valid(lib):
         (lambda d: setattr(d, 'io_dtype', 7), _lib.NXA_E_DTYPE, 'io_dtype'),
         (lambda d: setattr(d, 'bias_dtype', 9), _lib.NXA_E_DTYPE, 'bias_dtype'),
         (lambda d: setattr(d, 'Lq', 0), _lib.NXA_E_SHAPE, 'positive'),
-        (lambda d: setattr(d, 'D', 136), _lib.NXA_E_UNSUPPORTED, 'exceeds 128'),
+        (lambda d: setattr(d, 'D', 264), _lib.NXA_E_UNSUPPORTED, 'exceeds 256'),
         (lambda d: setattr(d, 'D', 12), _lib.NXA_E_UNSUPPORTED, 'multiple of 8'),
-        (lambda d: setattr(d, 'Dv', 136), _lib.NXA_E_UNSUPPORTED, 'Dv=136 exceeds 128'),
+        (lambda d: setattr(d, 'Dv', 264), _lib.NXA_E_UNSUPPORTED, 'Dv=264 exceeds 256'),
         (lambda d: setattr(d, 'Dv', 20), _lib.NXA_E_UNSUPPORTED, 'Dv=20 must be a multiple'),
         (lambda d: setattr(d, 'Dv', -8), _lib.NXA_E_SHAPE, 'negative'),
         (lambda d: d.q_str.__setitem__(2, 65), _lib.NXA_E_LAYOUT, 'stride'),

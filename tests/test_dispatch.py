@@ -147,9 +147,12 @@ def test_validate_raises_value_error(shapes):
         (torch.float64, 64, 64, False),
         (torch.bfloat16, 64, 32, True),
         (torch.float32, 64, 12, True),
-        (torch.bfloat16, 64, 136, False),
+        (torch.bfloat16, 64, 136, True),
+        (torch.bfloat16, 256, 256, True),
+        (torch.float32, 196, 128, True),
         (torch.bfloat16, 64, 20, False),
-        (torch.bfloat16, 136, 136, False),
+        (torch.bfloat16, 264, 264, False),
+        (torch.float16, 64, 512, False),
         (torch.bfloat16, 12, 12, False),
     ],
 )

@@ -165,6 +165,21 @@ def test_value_head_dim_differs(dtype, d, dv, kw):
 
 
 @pytest.mark.parametrize('dtype', DTYPES, ids=IDS)
+@pytest.mark.parametrize('d,dv,s,t,kw', [
+    (256, 256, 160, 150, {}),
+    (256, 256, 150, 150, {'causal': True}),
+    (192, 256, 130, 170, {'bias_shape': (2, 2, 130, 170), 'mask_kind': 'random'}),
+    (256, 64, 100, 136, {'bias_shape': (1, 2, 1, 136), 'mask_kind': 'keypad'}),
+    (136, 136, 70, 77, {'bias_shape': (2, 70, 77)}),
+], ids=['256', '256_causal', '192_256_bias_mask', '256_64_rowbias', '136_tails'])
+def test_wide_head_dim(dtype, d, dv, s, t, kw):
+    """Head dims above 128 (padded to 256): one wave per SIMD, narrower
+    tiles, dV / dK (and for fp32 dK / dQ column halves) in passes of their
+    own."""
+    _check(dtype, 2, 2, s, t, d, dv=dv, seed=40 + d + dv, **kw)
+
+
+@pytest.mark.parametrize('dtype', DTYPES, ids=IDS)
 @pytest.mark.parametrize('s,t', [(256, 256), (200, 130), (96, 300)])
 def test_causal(dtype, s, t):
     _check(dtype, 2, 2, s, t, 64, causal=True, seed=3)
