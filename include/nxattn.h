@@ -113,6 +113,23 @@ int nxa_bwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
             void* dbias, const int64_t* dbias_str, void* workspace,
             size_t workspace_bytes, int tilemap_ready, void* stream);
 
+/* qk-norm: y = x * rsqrt(mean(x^2) + eps) over each row of D elements, in
+ * fp32, written in `dtype` (the reference's qk_rms_norm, _reference.py:52-77,
+ * which the fused path applies in the I/O dtype before the kernel,
+ * nn/attention/__init__.py:196-197), with the per-row rsqrt kept in `rstd`
+ * (fp32, may be NULL).  Rows of x are x_stride elements apart (unit stride
+ * over D); y is [rows, D] contiguous.  D must be a multiple of 8 (bf16,
+ * fp16) or 4 (fp32) and the pointers 16-byte aligned.  One pass, HBM-bound. */
+int nxa_rms_norm_fwd(int64_t rows, int32_t D, int32_t dtype, const void* x,
+                     int64_t x_stride, void* y, float* rstd, float eps,
+                     void* stream);
+
+/* VJP of nxa_rms_norm_fwd: dx = r * (dy - y * mean(dy * y)) with r = rstd
+ * and y = x * r in fp32; dy and dx are [rows, D] contiguous. */
+int nxa_rms_norm_bwd(int64_t rows, int32_t D, int32_t dtype, const void* x,
+                     int64_t x_stride, const void* dy, const float* rstd,
+                     void* dx, void* stream);
+
 /* Message of the last failure on this thread ("" if none). */
 const char* nxa_last_error(void);
 
@@ -120,7 +137,7 @@ const char* nxa_last_error(void);
  * library launches is bracketed by HIP events on its stream; nxa_profile_read
  * waits for them and returns the summed milliseconds and launch count of the
  * kernels whose name starts with `kernel` ("fwd", "dkdv", "dq", "delta",
- * "tilemap", "dbias_reduce").  Not for concurrent use from several threads. */
+ * "tilemap", "dbias_reduce", "rms_norm_fwd", "rms_norm_bwd").  Not for concurrent use from several threads. */
 int nxa_profile_enable(int on);
 int nxa_profile_read(const char* kernel, double* total_ms, int64_t* launches);
 int nxa_profile_reset(void);

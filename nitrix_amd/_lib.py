@@ -44,6 +44,8 @@ EXPORTS = (
     'nxa_workspace_bytes',
     'nxa_fwd',
     'nxa_bwd',
+    'nxa_rms_norm_fwd',
+    'nxa_rms_norm_bwd',
     'nxa_last_error',
     'nxa_profile_enable',
     'nxa_profile_read',
@@ -112,6 +114,11 @@ def _declare(lib: ctypes.CDLL) -> None:
         ctypes.POINTER(ctypes.c_int64),  # dbias_str
         vp, ctypes.c_size_t, ctypes.c_int, vp,
     ]
+    i64, i32 = ctypes.c_int64, ctypes.c_int32
+    lib.nxa_rms_norm_fwd.restype = ctypes.c_int
+    lib.nxa_rms_norm_fwd.argtypes = [i64, i32, i32, vp, i64, vp, vp, ctypes.c_float, vp]
+    lib.nxa_rms_norm_bwd.restype = ctypes.c_int
+    lib.nxa_rms_norm_bwd.argtypes = [i64, i32, i32, vp, i64, vp, vp, vp, vp]
     lib.nxa_last_error.restype = ctypes.c_char_p
     lib.nxa_last_error.argtypes = []
     lib.nxa_profile_enable.restype = ctypes.c_int

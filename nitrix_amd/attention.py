@@ -79,6 +79,60 @@ def qk_rms_norm(z: torch.Tensor) -> torch.Tensor:
     return (zf * torch.rsqrt(ms + _QK_RMS_EPS)).to(z.dtype)
 
 
+class _RmsNormHip(torch.autograd.Function):
+    """qk-norm in one HIP pass per direction (``nxa_rms_norm_fwd`` /
+    ``nxa_rms_norm_bwd``): the same math as :func:`qk_rms_norm` (fp32, cast
+    back to ``x.dtype``), without its fp32 temporaries."""
+
+    @staticmethod
+    def forward(ctx, x):
+        d = x.shape[-1]
+        epc = 4 if x.dtype == torch.float32 else 8
+        x2 = x.reshape(-1, d)
+        if x2.stride(-1) != 1 or x2.data_ptr() % 16 or x2.stride(0) % epc:
+            x2 = x2.contiguous()
+        rows = x2.shape[0]
+        y = torch.empty((rows, d), dtype=x.dtype, device=x.device)
+        rstd = torch.empty((rows,), dtype=torch.float32, device=x.device)
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        _lib.check(
+            _lib.lib().nxa_rms_norm_fwd(
+                rows, d, _IO_DTYPES[x.dtype], x2.data_ptr(), x2.stride(0),
+                y.data_ptr(), rstd.data_ptr(), _QK_RMS_EPS, stream,
+            )
+        )
+        ctx.save_for_backward(x2, rstd)
+        ctx.shape = x.shape
+        return y.reshape(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, rstd = ctx.saved_tensors
+        rows, d = x2.shape
+        dy2 = dy.reshape(rows, d)
+        if not dy2.is_contiguous() or dy2.data_ptr() % 16:
+            dy2 = dy2.contiguous()
+        dx = torch.empty((rows, d), dtype=x2.dtype, device=x2.device)
+        stream = torch.cuda.current_stream(x2.device).cuda_stream
+        _lib.check(
+            _lib.lib().nxa_rms_norm_bwd(
+                rows, d, _IO_DTYPES[x2.dtype], x2.data_ptr(), x2.stride(0),
+                dy2.data_ptr(), rstd.data_ptr(), dx.data_ptr(), stream,
+            )
+        )
+        return dx.reshape(ctx.shape)
+
+
+def _qk_norm_fused(z: torch.Tensor) -> torch.Tensor:
+    """qk-norm on the fused path: the one-pass HIP kernels for GPU tensors of
+    a kernel dtype whose head dim fits their 16-byte loads, else
+    :func:`qk_rms_norm`."""
+    epc = 4 if z.dtype == torch.float32 else 8
+    if z.is_cuda and z.dtype in _IO_DTYPES and z.numel() > 0 and z.shape[-1] % epc == 0:
+        return _RmsNormHip.apply(z)
+    return qk_rms_norm(z)
+
+
 def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
     """``__init__.py:40-60``: same checks, same exception type."""
     if q.ndim < 3 or k.ndim < 3 or v.ndim < 3:
@@ -500,8 +554,8 @@ def scaled_dot_product_attention(
     resolved_scale = default_scale(q.shape[-1]) if scale is None else scale
     resolved = resolve_backend(backend, q.device)
     if resolved == 'hip':
-        q_in = qk_rms_norm(q) if qk_norm else q
-        k_in = qk_rms_norm(k) if qk_norm else k
+        q_in = _qk_norm_fused(q) if qk_norm else q
+        k_in = _qk_norm_fused(k) if qk_norm else k
         try:
             return scaled_dot_product_attention_hip(
                 q_in,

@@ -332,6 +332,31 @@ int check_io_ptrs(const nxa_desc* d, const void* const* ptrs, const char* const*
   return NXA_OK;
 }
 
+// Validation of the qk-norm entry points.
+int check_norm(int64_t rows, int32_t D, int32_t dtype, const void* x, int64_t x_stride,
+               const void* const* ptrs, const char* const* names, int n) {
+  if (!known_dtype(dtype))
+    return fail(NXA_E_DTYPE, "dtype %d is not NXA_BF16, NXA_F16 or NXA_F32", dtype);
+  if (rows <= 0 || D <= 0)
+    return fail(NXA_E_SHAPE, "rms norm needs rows > 0 and D > 0 (rows=%lld D=%d)",
+                (long long)rows, D);
+  if (rows > ((int64_t)1 << 31) * 16)
+    return fail(NXA_E_SHAPE, "rms norm: %lld rows exceed the grid", (long long)rows);
+  const int epc = 16 / esize(dtype);
+  if (D % epc != 0)
+    return fail(NXA_E_UNSUPPORTED, "rms norm: D=%d must be a multiple of %d", D, epc);
+  if (x_stride < D || x_stride % epc != 0)
+    return fail(NXA_E_LAYOUT, "rms norm: row stride %lld must be >= D and a multiple of %d",
+                (long long)x_stride, epc);
+  if (!x) return fail(NXA_E_ARG, "x is NULL");
+  if (!aligned(x, 16)) return fail(NXA_E_LAYOUT, "x is not 16-byte aligned");
+  for (int i = 0; i < n; ++i) {
+    if (!ptrs[i]) return fail(NXA_E_ARG, "%s is NULL", names[i]);
+    if (!aligned(ptrs[i], 16)) return fail(NXA_E_LAYOUT, "%s is not 16-byte aligned", names[i]);
+  }
+  return NXA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -457,6 +482,44 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
     if (rc) return rc;
   }
   return NXA_OK;
+}
+
+int nxa_rms_norm_fwd(int64_t rows, int32_t D, int32_t dtype, const void* x,
+                     int64_t x_stride, void* y, float* rstd, float eps, void* stream) {
+  const void* ptrs[1] = {y};
+  const char* names[1] = {"y"};
+  int rc = check_norm(rows, D, dtype, x, x_stride, ptrs, names, 1);
+  if (rc) return rc;
+  if (!(eps >= 0.f)) return fail(NXA_E_ARG, "rms norm: eps must be >= 0");
+  nxa::NormParams p{};
+  p.x = x;
+  p.y = y;
+  p.rstd = rstd;
+  p.rows = rows;
+  p.x_stride = x_stride;
+  p.D = D;
+  p.eps = eps;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  return launch("rms_norm_fwd", s, [&] { nxa::launch_rms_norm(p, dtype, false, s); });
+}
+
+int nxa_rms_norm_bwd(int64_t rows, int32_t D, int32_t dtype, const void* x,
+                     int64_t x_stride, const void* dy, const float* rstd, void* dx,
+                     void* stream) {
+  const void* ptrs[3] = {dy, rstd, dx};
+  const char* names[3] = {"dy", "rstd", "dx"};
+  int rc = check_norm(rows, D, dtype, x, x_stride, ptrs, names, 3);
+  if (rc) return rc;
+  nxa::NormParams p{};
+  p.x = x;
+  p.rstd = const_cast<float*>(rstd);
+  p.dy = dy;
+  p.dx = dx;
+  p.rows = rows;
+  p.x_stride = x_stride;
+  p.D = D;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  return launch("rms_norm_bwd", s, [&] { nxa::launch_rms_norm(p, dtype, true, s); });
 }
 
 int nxa_profile_enable(int on) {

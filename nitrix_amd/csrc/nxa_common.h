@@ -96,6 +96,18 @@ struct Params {
   float bias_h, bias_l;  // 1/scale = bias_h + bias_l, both exact in the bias dtype
 };
 
+// Parameter block of the qk-norm kernels.
+struct NormParams {
+  const void* x;        // rows of D elements, x_stride apart
+  void* y;              // forward output [rows, D]
+  float* rstd;          // per-row rsqrt(mean(x^2) + eps)
+  const void* dy;       // backward: cotangent of y [rows, D]
+  void* dx;             // backward output [rows, D]
+  int64_t rows, x_stride;
+  int D;
+  float eps;
+};
+
 // How the 16-bit forward adds the bias (chosen on the host).
 //  * kFbRow  / kFbTile: the bias enters the score accumulator through MFMA
 //    products bias^T x diag(1/scale) (1/scale split into two terms of the

@@ -16,6 +16,7 @@ void launch_dkdv(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dkdv16(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dq16(const Params& p, int io_dtype, int dp, hipStream_t stream);
+void launch_rms_norm(const NormParams& p, int dtype, bool bwd, hipStream_t stream);
 void launch_dbias_reduce(const Params& p, void* out, const int64_t* out_str,
                          int OB, int OH, int LQ, hipStream_t stream);
 

@@ -267,6 +267,32 @@ def test_backward_fd_value_head_dim_differs(dv):
     _fd_check(lambda s, t: (2, 2, s, t), causal=True, with_mask=True, dv=dv)
 
 
+def test_qk_rms_norm_vjp_matches_finite_differences():
+    rng = np.random.RandomState(5)
+    z = rng.standard_normal((3, 2, 7))
+    z[1, 0] *= 1e-4  # a row whose mean square is near eps
+    g = rng.standard_normal((3, 2, 7))
+    got = O.qk_rms_norm_vjp(z, g)
+    eps = 1e-6
+    fd = np.zeros_like(z)
+    for idx in np.ndindex(z.shape):
+        zp = z.copy()
+        zp[idx] += eps
+        zm = z.copy()
+        zm[idx] -= eps
+        fd[idx] = (np.sum(O.qk_rms_norm(zp) * g) - np.sum(O.qk_rms_norm(zm) * g)) / (2 * eps)
+    np.testing.assert_allclose(got, fd, atol=1e-7, rtol=1e-6)
+
+
+def test_qk_rms_norm_vjp_is_orthogonal_to_the_input():
+    # The output is invariant to scaling z (up to eps), so the cotangent has
+    # no component along z: <z, dz> = 0 up to an O(eps / ms) term.
+    rng = np.random.RandomState(6)
+    z = rng.standard_normal((4, 16))
+    dz = O.qk_rms_norm_vjp(z, rng.standard_normal((4, 16)))
+    assert np.max(np.abs(np.sum(z * dz, axis=-1))) < 1e-5
+
+
 # --- bf16 semantics -----------------------------------------------------------
 
 
