@@ -90,6 +90,11 @@ CONFIGS = {
         bwd=True,
         workload='fp16 attention fwd+bwd, key-padding mask (C2 in fp16)',
     ),
+    'c2qk': dict(
+        io='bf16', B=8, H=16, L=4096, D=128, bias=None, mask='keypad', causal=False,
+        bwd=True, qk_norm=True,
+        workload='bf16 attention fwd+bwd with qk_norm, key-padding mask (C2 with qk-norm)',
+    ),
     'w256': dict(
         io='bf16', B=4, H=16, L=4096, D=256, bias=None, mask=None, causal=False,
         bwd=True,
@@ -277,11 +282,11 @@ class Workload:
                 if t is not None:
                     t.grad = None
             out = sdpa(self.q, self.k, self.v, bias=self.bias, mask=self.mask,
-                       causal=c['causal'], backend='hip')
+                       causal=c['causal'], qk_norm=c.get('qk_norm', False), backend='hip')
             out.backward(self.dout)
         else:
             sdpa(self.q, self.k, self.v, bias=self.bias, mask=self.mask,
-                 causal=c['causal'], backend='hip')
+                 causal=c['causal'], qk_norm=c.get('qk_norm', False), backend='hip')
 
     def check_finite(self, torch):
         if self.cfg['bwd']:
@@ -368,7 +373,8 @@ def main() -> int:
     torch.cuda.synchronize()
     _lib.profile_enable(False)
     kernels = {}
-    for kname in ('tilemap', 'fwd', 'delta', 'dkdv', 'dq', 'dbias_reduce'):
+    for kname in ('tilemap', 'fwd', 'delta', 'dkdv', 'dq', 'dbias_reduce',
+                  'rms_norm_fwd', 'rms_norm_bwd'):
         tot, n = _lib.profile_read(kname)
         if n:
             kernels[kname] = {'avg_ms': tot / n, 'launches_per_step': n / prof_steps}
