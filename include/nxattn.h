@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define NXA_VERSION 2
+#define NXA_VERSION 3
 
 typedef enum { NXA_BF16 = 0, NXA_F32 = 1, NXA_F16 = 2 } nxa_dtype;
 
@@ -130,6 +130,43 @@ int nxa_rms_norm_bwd(int64_t rows, int32_t D, int32_t dtype, const void* x,
                      int64_t x_stride, const void* dy, const float* rstd,
                      void* dx, void* stream);
 
+/* Selective state-space scan (Mamba / S6), fp32.  The counterpart of the
+ * fused selective scan the reference dispatches to at
+ *   src/nitrix/nn/ssm/__init__.py:81-124        (_selective_scan_pallas)
+ *   src/nitrix/_kernels/cuda/selective_scan.py:497-549 (selective_scan_pallas)
+ * one for one:
+ *   nxa_ssm_check            <- _check_tileable / _resolve_chunk  :463-494
+ *   nxa_ssm_fwd              <- _fused_forward + _mha_like_forward :119-233
+ *                               (y and the saved chunk-start states, hstart)
+ *   nxa_ssm_bwd              <- _fused_backward + _mha_like_backward :324-419
+ *                               (dx, ddelta, dA, dB, dC, dD; dA / dD summed
+ *                               over the batch as the reference's partials)
+ *   nxa_ssm_state_bytes,
+ *   nxa_ssm_workspace_bytes  <- (XLA buffers of the reference; caller-owned
+ *                               here)
+ * Layout: x, delta, y, dy, dx, ddelta [nb, L, d]; B, C, dB, dC [nb, L, n];
+ * A, dA [d, n]; D, dD [d]; contiguous fp32, 4-byte aligned; leading batch
+ * axes pre-flattened into nb.  h_t = exp(delta_t A) h_{t-1} + delta_t B_t x_t
+ * from h = 0 and y_t = C_t . h_t (+ D x_t), per (batch, channel).  Any L >= 1,
+ * 1 <= n <= 32 (else NXA_E_UNSUPPORTED).  D may be NULL (no skip term; dD is
+ * then not written).  `state` (nxa_ssm_state_bytes) receives the state
+ * entering every 8-step sub-chunk, which nxa_ssm_bwd reads; it may be NULL
+ * in nxa_ssm_fwd when no backward follows.  The workspace (256-byte aligned,
+ * nxa_ssm_workspace_bytes) is scratch for one call.  dA, dB, dC, dD are
+ * overwritten (not accumulated), deterministically (fixed-order sums). */
+int nxa_ssm_check(int64_t nb, int32_t L, int32_t d, int32_t n);
+size_t nxa_ssm_state_bytes(int64_t nb, int32_t L, int32_t d, int32_t n);
+size_t nxa_ssm_workspace_bytes(int64_t nb, int32_t L, int32_t d, int32_t n, int is_bwd);
+int nxa_ssm_fwd(int64_t nb, int32_t L, int32_t d, int32_t n, const float* x,
+                const float* delta, const float* A, const float* B, const float* C,
+                const float* D, float* y, float* state, void* workspace,
+                size_t workspace_bytes, void* stream);
+int nxa_ssm_bwd(int64_t nb, int32_t L, int32_t d, int32_t n, const float* x,
+                const float* delta, const float* A, const float* B, const float* C,
+                const float* D, const float* state, const float* dy, float* dx,
+                float* ddelta, float* dA, float* dB, float* dC, float* dD,
+                void* workspace, size_t workspace_bytes, void* stream);
+
 /* Message of the last failure on this thread ("" if none). */
 const char* nxa_last_error(void);
 
@@ -137,7 +174,8 @@ const char* nxa_last_error(void);
  * library launches is bracketed by HIP events on its stream; nxa_profile_read
  * waits for them and returns the summed milliseconds and launch count of the
  * kernels whose name starts with `kernel` ("fwd", "dkdv", "dq", "delta",
- * "tilemap", "dbias_reduce", "rms_norm_fwd", "rms_norm_bwd").  Not for concurrent use from several threads. */
+ * "tilemap", "dbias_reduce", "rms_norm_fwd", "rms_norm_bwd", "ssm_fwd",
+ * "ssm_bwd"; the last two cover a whole scan pass, several kernels).  Not for concurrent use from several threads. */
 int nxa_profile_enable(int on);
 int nxa_profile_read(const char* kernel, double* total_ms, int64_t* launches);
 int nxa_profile_reset(void);

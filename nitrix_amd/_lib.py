@@ -46,6 +46,11 @@ EXPORTS = (
     'nxa_bwd',
     'nxa_rms_norm_fwd',
     'nxa_rms_norm_bwd',
+    'nxa_ssm_check',
+    'nxa_ssm_state_bytes',
+    'nxa_ssm_workspace_bytes',
+    'nxa_ssm_fwd',
+    'nxa_ssm_bwd',
     'nxa_last_error',
     'nxa_profile_enable',
     'nxa_profile_read',
@@ -119,6 +124,16 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.nxa_rms_norm_fwd.argtypes = [i64, i32, i32, vp, i64, vp, vp, ctypes.c_float, vp]
     lib.nxa_rms_norm_bwd.restype = ctypes.c_int
     lib.nxa_rms_norm_bwd.argtypes = [i64, i32, i32, vp, i64, vp, vp, vp, vp]
+    lib.nxa_ssm_check.restype = ctypes.c_int
+    lib.nxa_ssm_check.argtypes = [i64, i32, i32, i32]
+    lib.nxa_ssm_state_bytes.restype = ctypes.c_size_t
+    lib.nxa_ssm_state_bytes.argtypes = [i64, i32, i32, i32]
+    lib.nxa_ssm_workspace_bytes.restype = ctypes.c_size_t
+    lib.nxa_ssm_workspace_bytes.argtypes = [i64, i32, i32, i32, ctypes.c_int]
+    lib.nxa_ssm_fwd.restype = ctypes.c_int
+    lib.nxa_ssm_fwd.argtypes = [i64, i32, i32, i32] + [vp] * 9 + [ctypes.c_size_t, vp]
+    lib.nxa_ssm_bwd.restype = ctypes.c_int
+    lib.nxa_ssm_bwd.argtypes = [i64, i32, i32, i32] + [vp] * 15 + [ctypes.c_size_t, vp]
     lib.nxa_last_error.restype = ctypes.c_char_p
     lib.nxa_last_error.argtypes = []
     lib.nxa_profile_enable.restype = ctypes.c_int

@@ -357,6 +357,55 @@ int check_norm(int64_t rows, int32_t D, int32_t dtype, const void* x, int64_t x_
   return NXA_OK;
 }
 
+// Selective scan: extents, limits and workspace layout.
+constexpr int kSsmMaxStates = 32;
+
+struct SsmLayout {
+  int NP, nc, ns, ndblk;
+  size_t hc, sdt, gc, dD, dBC;  // byte sizes of the workspace parts
+  size_t state;                 // byte size of the saved sub-chunk states
+};
+
+SsmLayout ssm_layout(int64_t nb, int32_t L, int32_t Dm, int32_t N) {
+  SsmLayout s;
+  s.NP = nxa::ssm_padded_states(N);
+  s.nc = (L + nxa::kSsmChunk - 1) / nxa::kSsmChunk;
+  s.ns = (L + nxa::kSsmSub - 1) / nxa::kSsmSub;
+  s.ndblk = (Dm + nxa::kSsmBlock - 1) / nxa::kSsmBlock;
+  const size_t f = sizeof(float);
+  s.hc = align256((size_t)nb * s.nc * s.NP * Dm * f);
+  s.gc = s.hc;
+  s.sdt = align256((size_t)nb * s.nc * Dm * f);
+  s.dD = s.sdt;
+  s.dBC = align256((size_t)s.ndblk * nb * L * 2 * s.NP * f);
+  s.state = (size_t)nb * s.ns * s.NP * Dm * f;
+  return s;
+}
+
+int check_ssm(int64_t nb, int32_t L, int32_t Dm, int32_t N) {
+  if (nb <= 0 || L <= 0 || Dm <= 0 || N <= 0)
+    return fail(NXA_E_SHAPE, "selective scan: extents must be positive (nb=%lld L=%d d=%d n=%d)",
+                (long long)nb, L, Dm, N);
+  if (N > kSsmMaxStates)
+    return fail(NXA_E_UNSUPPORTED, "selective scan: state dim n=%d exceeds %d", N,
+                kSsmMaxStates);
+  const SsmLayout s = ssm_layout(nb, L, Dm, N);
+  if ((int64_t)s.ndblk * s.nc * nb >= ((int64_t)1 << 31) ||
+      nb * s.NP * (int64_t)Dm >= ((int64_t)1 << 38))
+    return fail(NXA_E_SHAPE, "selective scan: nb=%lld L=%d d=%d exceed the grid",
+                (long long)nb, L, Dm);
+  return NXA_OK;
+}
+
+int check_ptrs(const void* const* ptrs, const char* const* names, int n) {
+  for (int i = 0; i < n; ++i) {
+    if (!ptrs[i]) return fail(NXA_E_ARG, "selective scan: %s is NULL", names[i]);
+    if (!aligned(ptrs[i], 4))
+      return fail(NXA_E_LAYOUT, "selective scan: %s is not 4-byte aligned", names[i]);
+  }
+  return NXA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -520,6 +569,108 @@ int nxa_rms_norm_bwd(int64_t rows, int32_t D, int32_t dtype, const void* x,
   p.D = D;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   return launch("rms_norm_bwd", s, [&] { nxa::launch_rms_norm(p, dtype, true, s); });
+}
+
+int nxa_ssm_check(int64_t nb, int32_t L, int32_t d, int32_t n) {
+  return check_ssm(nb, L, d, n);
+}
+
+size_t nxa_ssm_state_bytes(int64_t nb, int32_t L, int32_t d, int32_t n) {
+  if (check_ssm(nb, L, d, n)) return 0;
+  return ssm_layout(nb, L, d, n).state;
+}
+
+size_t nxa_ssm_workspace_bytes(int64_t nb, int32_t L, int32_t d, int32_t n, int is_bwd) {
+  if (check_ssm(nb, L, d, n)) return 0;
+  const SsmLayout s = ssm_layout(nb, L, d, n);
+  return is_bwd ? s.gc + s.sdt + s.dD + s.dBC : s.hc + s.sdt;
+}
+
+int nxa_ssm_fwd(int64_t nb, int32_t L, int32_t d, int32_t n, const float* x,
+                const float* delta, const float* A, const float* B, const float* C,
+                const float* D, float* y, float* state, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  int rc = check_ssm(nb, L, d, n);
+  if (rc) return rc;
+  const void* ptrs[7] = {x, delta, A, B, C, y, workspace};
+  const char* names[7] = {"x", "delta", "A", "B", "C", "y", "workspace"};
+  if ((rc = check_ptrs(ptrs, names, 7))) return rc;
+  if ((D && !aligned(D, 4)) || (state && !aligned(state, 4)))
+    return fail(NXA_E_LAYOUT, "selective scan: D / state not 4-byte aligned");
+  const SsmLayout s = ssm_layout(nb, L, d, n);
+  if (workspace_bytes < s.hc + s.sdt || !aligned(workspace, 256))
+    return fail(NXA_E_WORKSPACE, "selective scan: workspace needs %zu bytes, 256-byte aligned",
+                s.hc + s.sdt);
+  nxa::SsmParams p{};
+  p.x = x;
+  p.delta = delta;
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  p.D = D;
+  p.y = y;
+  p.hs = state;
+  char* ws = static_cast<char*>(workspace);
+  p.hc = reinterpret_cast<float*>(ws);
+  p.sdt = reinterpret_cast<float*>(ws + s.hc);
+  p.nb = nb;
+  p.L = L;
+  p.Dm = d;
+  p.N = n;
+  p.nc = s.nc;
+  p.ns = s.ns;
+  p.ndblk = s.ndblk;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  return launch("ssm_fwd", st, [&] { nxa::launch_ssm(p, false, st); });
+}
+
+int nxa_ssm_bwd(int64_t nb, int32_t L, int32_t d, int32_t n, const float* x,
+                const float* delta, const float* A, const float* B, const float* C,
+                const float* D, const float* state, const float* dy, float* dx,
+                float* ddelta, float* dA, float* dB, float* dC, float* dD,
+                void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_ssm(nb, L, d, n);
+  if (rc) return rc;
+  const void* ptrs[13] = {x, delta, A, B, C, state, dy, dx, ddelta, dA, dB, dC, workspace};
+  const char* names[13] = {"x", "delta", "A", "B", "C", "state", "dy",
+                           "dx", "ddelta", "dA", "dB", "dC", "workspace"};
+  if ((rc = check_ptrs(ptrs, names, 13))) return rc;
+  if ((D && !aligned(D, 4)) || (dD && !aligned(dD, 4)))
+    return fail(NXA_E_LAYOUT, "selective scan: D / dD not 4-byte aligned");
+  const SsmLayout s = ssm_layout(nb, L, d, n);
+  const size_t need = s.gc + s.sdt + s.dD + s.dBC;
+  if (workspace_bytes < need || !aligned(workspace, 256))
+    return fail(NXA_E_WORKSPACE, "selective scan: workspace needs %zu bytes, 256-byte aligned",
+                need);
+  nxa::SsmParams p{};
+  p.x = x;
+  p.delta = delta;
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  p.D = D;
+  p.hs = const_cast<float*>(state);
+  p.dy = dy;
+  p.dx = dx;
+  p.ddelta = ddelta;
+  p.dA = dA;
+  p.dB = dB;
+  p.dC = dC;
+  p.dD = D ? dD : nullptr;
+  char* ws = static_cast<char*>(workspace);
+  p.gc = reinterpret_cast<float*>(ws);
+  p.sdt = reinterpret_cast<float*>(ws + s.gc);
+  p.dDpart = reinterpret_cast<float*>(ws + s.gc + s.sdt);
+  p.dBCpart = reinterpret_cast<float*>(ws + s.gc + s.sdt + s.dD);
+  p.nb = nb;
+  p.L = L;
+  p.Dm = d;
+  p.N = n;
+  p.nc = s.nc;
+  p.ns = s.ns;
+  p.ndblk = s.ndblk;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  return launch("ssm_bwd", st, [&] { nxa::launch_ssm(p, true, st); });
 }
 
 int nxa_profile_enable(int on) {

@@ -108,6 +108,24 @@ struct NormParams {
   float eps;
 };
 
+// Parameter block of the selective-scan kernels (fp32; layouts in nxa_ssm.hip).
+struct SsmParams {
+  const float *x, *delta, *A, *B, *C, *D;  // D may be null
+  float* y;
+  const float* dy;
+  float *dx, *ddelta, *dA, *dB, *dC, *dD;  // dD may be null
+  float* hc;      // [nb][nc][NP][Dm] chunk states: local end state, then entering state
+  float* gc;      // [nb][nc][NP][Dm] chunk adjoints, then the dA partial sums
+  float* sdt;     // [nb][nc][Dm] sum of delta over each chunk
+  float* hs;      // [nb][ns][NP][Dm] state entering each sub-chunk (may be null in fwd)
+  float* dDpart;  // [nb][nc][Dm]
+  float* dBCpart; // [ndblk][nb][L][2 NP]
+  int64_t nb;
+  int L, Dm, N;
+  int nc, ns;     // chunks, sub-chunks
+  int ndblk;      // channel blocks
+};
+
 // How the 16-bit forward adds the bias (chosen on the host).
 //  * kFbRow  / kFbTile: the bias enters the score accumulator through MFMA
 //    products bias^T x diag(1/scale) (1/scale split into two terms of the

@@ -17,6 +17,11 @@ void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dkdv16(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dq16(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_rms_norm(const NormParams& p, int dtype, bool bwd, hipStream_t stream);
+int ssm_padded_states(int N);
+constexpr int kSsmChunk = 32;   // steps per chunk of the selective scan
+constexpr int kSsmSub = 8;      // steps per saved sub-chunk state
+constexpr int kSsmBlock = 256;  // channels per block of the selective scan
+void launch_ssm(const SsmParams& p, bool bwd, hipStream_t stream);
 void launch_dbias_reduce(const Params& p, void* out, const int64_t* out_str,
                          int OB, int OH, int LQ, hipStream_t stream);
 
