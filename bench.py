@@ -18,6 +18,10 @@ The other BASELINE configurations are available as ``--config c1|c3|c4|c5``
   from 128x128 blocks kept with p=0.25 (diagonal kept), bias [1,8,1,L]
   (with its gradient).
 
+``--config ssm`` measures the sibling fused selective scan instead (fp32
+fwd+bwd, batch 8, L 2048, d 1536, n 16), in (batch, step, channel) elements
+per second, with its compulsory HBM bytes for the roofline.
+
 Counted FLOPs follow the flash-attention convention over *kept* (query, key)
 pairs only: 4*D per pair forward (QK^T, PV) and 10*D backward.  ``value`` is
 counted TFLOP/s of the whole step.
@@ -104,6 +108,12 @@ CONFIGS = {
         io='f32', B=1, H=16, L=2048, D=256, bias=None, mask=None, causal=False,
         bwd=True,
         workload='fp32 attention fwd+bwd, head dim 256',
+    ),
+    # The sibling fused kernel (selective scan), its own metric.
+    'ssm': dict(
+        io='f32', B=8, L=2048, Dm=1536, N=16, bwd=True,
+        workload='fp32 selective scan fwd+bwd (Mamba-sized: batch 8, L 2048, '
+        'd 1536, n 16, with D; delta in [0.01, 0.1], A = -(1..n))',
     ),
 }
 
@@ -294,6 +304,170 @@ class Workload:
                 assert torch.isfinite(t.grad.float()).all(), 'non-finite gradient'
 
 
+def _ssm_bytes(B, L, Dm, N):
+    """Compulsory HBM bytes of one selective-scan step (fp32): forward reads
+    x, delta, B, C, A, D and writes y; backward reads x, delta, dy, B, C, A, D
+    and writes dx, ddelta, dB, dC, dA, dD."""
+    xd = B * L * Dm * 4
+    bc = B * L * N * 4
+    par = (Dm * N + Dm) * 4
+    fwd = 3 * xd + 2 * bc + par
+    bwd = 5 * xd + 4 * bc + 2 * par
+    return fwd, bwd
+
+
+def _ssm_cpu_baseline(cfg, budget_s: float = 12.0):
+    """Oracle forward + VJP on (1, L, 64)-channel slices of the workload until
+    ~budget_s of CPU time, in the GPU line's unit."""
+    from oracle import ssm as S
+
+    L, N = cfg['L'], cfg['N']
+    rng = np.random.Generator(np.random.PCG64(SEED + 3))
+    dm = 64
+
+    def sample():
+        x = rng.standard_normal((1, L, dm)).astype(np.float32)
+        delta = (0.01 + 0.09 / (1 + np.exp(-rng.standard_normal((1, L, dm))))).astype(np.float32)
+        A = -np.repeat((np.arange(N) + 1.0)[None, :], dm, 0).astype(np.float32)
+        B = rng.standard_normal((1, L, N)).astype(np.float32)
+        C = rng.standard_normal((1, L, N)).astype(np.float32)
+        D = rng.standard_normal((dm,)).astype(np.float32)
+        dy = rng.standard_normal((1, L, dm)).astype(np.float32)
+        return x, delta, A, B, C, D, dy
+
+    samples = [sample() for _ in range(2)]
+    n = 0
+    dt = 0.0
+    while dt < budget_s:
+        x, delta, A, B, C, D, dy = samples[n % 2]
+        t0 = time.perf_counter()
+        S.selective_scan(x, delta, A, B, C, D)
+        S.selective_scan_vjp(x, delta, A, B, C, D, dy, acc_dtype=np.float32)
+        dt += time.perf_counter() - t0
+        n += 1
+    return {
+        'value': n * L * dm / dt / 1e9,
+        'unit': 'Gelem/s',
+        'cores': int(_blas_threads()),
+        'kind': 'port',
+        'sample': (
+            f'{n} slices of 1 x {L} steps x {dm} channels x {N} states of the ssm workload, '
+            f'numpy oracle forward + VJP in float32, {dt:.1f} s'
+        ),
+    }
+
+
+def _bench_ssm(args, torch) -> int:
+    """Selective scan fwd+bwd through the public drop-in (autograd over the
+    C ABI); value = (batch, step, channel) elements per second."""
+    from nitrix_amd import _lib, selective_scan
+
+    _lib.lib()
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    cfg = CONFIGS['ssm']
+    Bn, L, Dm, N = cfg['B'], cfg['L'], cfg['Dm'], cfg['N']
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32)
+
+    x = randn(Bn, L, Dm).requires_grad_(True)
+    delta = (0.01 + 0.09 * torch.sigmoid(randn(Bn, L, Dm))).requires_grad_(True)
+    A = (-(torch.arange(N, device=dev, dtype=torch.float32) + 1.0)).repeat(Dm, 1)
+    A.requires_grad_(True)
+    Bm = randn(Bn, L, N).requires_grad_(True)
+    Cm = randn(Bn, L, N).requires_grad_(True)
+    Dv = randn(Dm).requires_grad_(True)
+    dy = randn(Bn, L, Dm)
+    leaves = (x, delta, A, Bm, Cm, Dv)
+
+    def step():
+        for t in leaves:
+            t.grad = None
+        y = selective_scan(x, delta, A, Bm, Cm, Dv, backend='hip')
+        y.backward(dy)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    assert all(torch.isfinite(t.grad).all() for t in leaves), 'non-finite gradient'
+    stream = torch.cuda.current_stream(dev)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    ms = e0.elapsed_time(e1) / args.steps
+    elems = Bn * L * Dm
+    value = elems / (ms * 1e-3) / 1e9
+
+    prof_steps = max(3, min(args.steps, 10))
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    for _ in range(prof_steps):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    kernels = {}
+    for kname in ('ssm_fwd', 'ssm_bwd'):
+        tot, n = _lib.profile_read(kname)
+        if n:
+            kernels[kname] = {'avg_ms': tot / n, 'launches_per_step': n / prof_steps}
+    _lib.profile_reset()
+    fwd_b, bwd_b = _ssm_bytes(Bn, L, Dm, N)
+    # The backward pass (five kernels) dominates; its compulsory bytes over
+    # its measured duration.
+    bwd_s = kernels['ssm_bwd']['avg_ms'] * 1e-3
+    achieved = bwd_b / bwd_s / 1e9
+    roofline = {
+        'kernel': 'ssm_bwd (backward pass: local, carry, chunk, two reductions)',
+        'bound': 'hbm',
+        'achieved': round(achieved, 2),
+        'peak': PEAK_HBM_GBS,
+        'unit': 'GB/s',
+        'frac': round(achieved / PEAK_HBM_GBS, 4),
+        'traffic': None,
+        'algorithmic_bytes': int(bwd_b),
+    }
+    cpu = None if args.no_cpu_baseline else _ssm_cpu_baseline(cfg)
+    line = {
+        'metric': f'selective scan fwd+bwd Gelem/s at B{Bn} L{L} D{Dm} N{N} (fp32)',
+        'value': round(value, 3),
+        'unit': 'Gelem/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(ms, 4),
+        'wall_s_timed': round(wall, 4),
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'f32',
+        'data': 'synthetic',
+        'config': {
+            'workload': cfg['workload'],
+            'config_id': 'ssm',
+            'B': Bn, 'L': L, 'D': Dm, 'N': N,
+            'global_batch': Bn,
+            'seq_len': L,
+            'parallelism': 'single GPU',
+        },
+        'fwd_gbs': round(fwd_b / (kernels['ssm_fwd']['avg_ms'] * 1e-3) / 1e9, 2),
+        'kernels': {k_: {kk: round(vv, 5) for kk, vv in v_.items()} for k_, v_ in kernels.items()},
+        'roofline': roofline,
+        'cpu_baseline': cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -331,6 +505,9 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({'copy_calibration_bytes_per_copy': n}), flush=True)
         return 0
+
+    if args.config == 'ssm':
+        return _bench_ssm(args, torch)
 
     from nitrix_amd import _lib, scaled_dot_product_attention
 

@@ -361,7 +361,7 @@ int check_norm(int64_t rows, int32_t D, int32_t dtype, const void* x, int64_t x_
 constexpr int kSsmMaxStates = 32;
 
 struct SsmLayout {
-  int NP, nc, ns, ndblk;
+  int NP, nc, ns, ndblk, ndblk_b;
   size_t hc, sdt, gc, dD, dBC;  // byte sizes of the workspace parts
   size_t state;                 // byte size of the saved sub-chunk states
 };
@@ -372,12 +372,14 @@ SsmLayout ssm_layout(int64_t nb, int32_t L, int32_t Dm, int32_t N) {
   s.nc = (L + nxa::kSsmChunk - 1) / nxa::kSsmChunk;
   s.ns = (L + nxa::kSsmSub - 1) / nxa::kSsmSub;
   s.ndblk = (Dm + nxa::kSsmBlock - 1) / nxa::kSsmBlock;
+  const int cpb = nxa::kSsmBlock / nxa::ssm_lanes_per_channel(s.NP);
+  s.ndblk_b = (Dm + cpb - 1) / cpb;
   const size_t f = sizeof(float);
   s.hc = align256((size_t)nb * s.nc * s.NP * Dm * f);
   s.gc = s.hc;
   s.sdt = align256((size_t)nb * s.nc * Dm * f);
   s.dD = s.sdt;
-  s.dBC = align256((size_t)s.ndblk * nb * L * 2 * s.NP * f);
+  s.dBC = align256((size_t)s.ndblk_b * nb * L * 2 * s.NP * f);
   s.state = (size_t)nb * s.ns * s.NP * Dm * f;
   return s;
 }
@@ -390,7 +392,7 @@ int check_ssm(int64_t nb, int32_t L, int32_t Dm, int32_t N) {
     return fail(NXA_E_UNSUPPORTED, "selective scan: state dim n=%d exceeds %d", N,
                 kSsmMaxStates);
   const SsmLayout s = ssm_layout(nb, L, Dm, N);
-  if ((int64_t)s.ndblk * s.nc * nb >= ((int64_t)1 << 31) ||
+  if ((int64_t)s.ndblk_b * s.nc * nb >= ((int64_t)1 << 31) ||
       nb * s.NP * (int64_t)Dm >= ((int64_t)1 << 38))
     return fail(NXA_E_SHAPE, "selective scan: nb=%lld L=%d d=%d exceed the grid",
                 (long long)nb, L, Dm);
@@ -669,6 +671,7 @@ int nxa_ssm_bwd(int64_t nb, int32_t L, int32_t d, int32_t n, const float* x,
   p.nc = s.nc;
   p.ns = s.ns;
   p.ndblk = s.ndblk;
+  p.ndblk_b = s.ndblk_b;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   return launch("ssm_bwd", st, [&] { nxa::launch_ssm(p, true, st); });
 }

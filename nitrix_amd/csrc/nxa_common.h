@@ -119,11 +119,12 @@ struct SsmParams {
   float* sdt;     // [nb][nc][Dm] sum of delta over each chunk
   float* hs;      // [nb][ns][NP][Dm] state entering each sub-chunk (may be null in fwd)
   float* dDpart;  // [nb][nc][Dm]
-  float* dBCpart; // [ndblk][nb][L][2 NP]
+  float* dBCpart; // [ndblk_b][nb][L][2 NP]
   int64_t nb;
   int L, Dm, N;
   int nc, ns;     // chunks, sub-chunks
-  int ndblk;      // channel blocks
+  int ndblk;      // channel blocks (one lane per channel)
+  int ndblk_b;    // channel blocks of the backward chunk pass (lanes per channel > 1)
 };
 
 // How the 16-bit forward adds the bias (chosen on the host).

@@ -18,6 +18,7 @@ void launch_dkdv16(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dq16(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_rms_norm(const NormParams& p, int dtype, bool bwd, hipStream_t stream);
 int ssm_padded_states(int N);
+int ssm_lanes_per_channel(int NP);
 constexpr int kSsmChunk = 32;   // steps per chunk of the selective scan
 constexpr int kSsmSub = 8;      // steps per saved sub-chunk state
 constexpr int kSsmBlock = 256;  // channels per block of the selective scan

@@ -30,7 +30,8 @@
 //           5. carry over chunks from the last: the adjoint entering each
 //              chunk from the right;
 //           6. each chunk again, sub-chunk by sub-chunk from the last: the
-//              forward states from the saved sub-chunk state (registers), then
+//              forward states from the saved sub-chunk state (registers; 16
+//              or 32 states are split over 2 or 4 lanes of a channel), then
 //              the reverse walk: dx, ddelta, and per-chunk partial sums of
 //              dA, dD (per lane) and dB, dC (over the block's channels:
 //              butterfly reduce-scatter across the wave, then LDS);
@@ -50,14 +51,16 @@ struct SsmBlock {
   int dblk, c, b, d, t0, t1;
 };
 
-__device__ __forceinline__ SsmBlock ssm_block(const SsmParams& p) {
+// Block -> (channel block, chunk, batch); `lpc` lanes per channel.
+__device__ __forceinline__ SsmBlock ssm_block(const SsmParams& p, int ndblk = 0, int lpc = 1) {
   SsmBlock k;
+  if (ndblk == 0) ndblk = p.ndblk;
   const int bid = blockIdx.x;
-  k.dblk = bid % p.ndblk;
-  const int rest = bid / p.ndblk;
+  k.dblk = bid % ndblk;
+  const int rest = bid / ndblk;
   k.c = rest % p.nc;
   k.b = rest / p.nc;
-  k.d = k.dblk * kSsmBlock + threadIdx.x;
+  k.d = k.dblk * (kSsmBlock / lpc) + threadIdx.x / lpc;
   k.t0 = k.c * kSsmChunk;
   k.t1 = min(p.L, k.t0 + kSsmChunk);
   return k;
@@ -70,28 +73,53 @@ __device__ __forceinline__ void load_al(const SsmParams& p, int d, bool ok, floa
   for (int n = 0; n < NP; ++n) al[n] = (ok && n < p.N) ? p.A[(int64_t)d * p.N + n] * kLog2e : 0.f;
 }
 
-__device__ __forceinline__ float row_val(const float* row, int n, int N) {
-  return n < N ? row[n] : 0.f;
+// The chunk's rows of a [nb, L, N] matrix (B or C) into LDS, zero-padded to
+// NP states and past the end of the sequence.  Every thread of the block
+// takes part; the caller synchronises.
+template <int NP>
+__device__ __forceinline__ void stage_rows(const SsmParams& p, const SsmBlock& k,
+                                           const float* src, float (*dst)[NP]) {
+  for (int e = threadIdx.x; e < kSsmChunk * NP; e += kSsmBlock) {
+    const int j = e / NP, n = e % NP, t = k.t0 + j;
+    dst[j][n] = (t < k.t1 && n < p.N) ? src[((int64_t)k.b * p.L + t) * p.N + n] : 0.f;
+  }
+}
+
+// The lane's values of a [nb, L, Dm] tensor over the chunk, all loads issued
+// at once (steps past the end are left unset and never read).
+__device__ __forceinline__ void load_chunk(const SsmParams& p, const SsmBlock& k, int d,
+                                           const float* src, float (&r)[kSsmChunk]) {
+  const float* base = src + ((int64_t)k.b * p.L + k.t0) * p.Dm + d;
+#pragma unroll
+  for (int j = 0; j < kSsmChunk; ++j)
+    if (k.t0 + j < k.t1) r[j] = base[(int64_t)j * p.Dm];
 }
 
 // (1) Local forward scan of a chunk from zero: end state and sum(delta).
 template <int NP>
 __global__ __launch_bounds__(kSsmBlock) void ssm_fwd_local_kernel(const SsmParams p) {
+  __shared__ float sB[kSsmChunk][NP];
   const SsmBlock k = ssm_block(p);
+  stage_rows<NP>(p, k, p.B, sB);
+  __syncthreads();
   if (k.d >= p.Dm) return;
+  float dr[kSsmChunk], xr[kSsmChunk];
+  load_chunk(p, k, k.d, p.delta, dr);
+  load_chunk(p, k, k.d, p.x, xr);
   float al[NP], h[NP];
   load_al<NP>(p, k.d, true, al);
 #pragma unroll
   for (int n = 0; n < NP; ++n) h[n] = 0.f;
   float sdt = 0.f;
-  for (int t = k.t0; t < k.t1; ++t) {
-    const int64_t xi = ((int64_t)k.b * p.L + t) * p.Dm + k.d;
-    const float dt = p.delta[xi], dx = dt * p.x[xi];
-    const float* Bt = p.B + ((int64_t)k.b * p.L + t) * p.N;
 #pragma unroll
-    for (int n = 0; n < NP; ++n)
-      h[n] = __builtin_fmaf(fexp2(dt * al[n]), h[n], dx * row_val(Bt, n, p.N));
-    sdt += dt;
+  for (int j = 0; j < kSsmChunk; ++j) {
+    if (k.t0 + j < k.t1) {
+      const float dt = dr[j], dx = dt * xr[j];
+#pragma unroll
+      for (int n = 0; n < NP; ++n)
+        h[n] = __builtin_fmaf(fexp2(dt * al[n]), h[n], dx * sB[j][n]);
+      sdt += dt;
+    }
   }
   const int64_t cb = ((int64_t)k.b * p.nc + k.c) * NP;
 #pragma unroll
@@ -123,40 +151,42 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_carry_kernel(const SsmParams p,
 }
 
 // (3) Output pass: each chunk from its entering state; y, and the state
-// entering each SC-step sub-chunk when p.hs is set.
+// entering each 8-step sub-chunk when p.hs is set.
 template <int NP>
 __global__ __launch_bounds__(kSsmBlock) void ssm_fwd_out_kernel(const SsmParams p) {
+  __shared__ float sB[kSsmChunk][NP], sC[kSsmChunk][NP];
   const SsmBlock k = ssm_block(p);
+  stage_rows<NP>(p, k, p.B, sB);
+  stage_rows<NP>(p, k, p.C, sC);
+  __syncthreads();
   if (k.d >= p.Dm) return;
+  float dr[kSsmChunk], xr[kSsmChunk];
+  load_chunk(p, k, k.d, p.delta, dr);
+  load_chunk(p, k, k.d, p.x, xr);
   float al[NP], h[NP];
   load_al<NP>(p, k.d, true, al);
   const int64_t cb = ((int64_t)k.b * p.nc + k.c) * NP;
 #pragma unroll
   for (int n = 0; n < NP; ++n) h[n] = p.hc[(cb + n) * p.Dm + k.d];
   const float Dd = p.D ? p.D[k.d] : 0.f;
-  constexpr int SC = kSsmSub;
-  for (int ts = k.t0; ts < k.t1; ts += SC) {
-    if (p.hs) {
-      const int64_t sb = ((int64_t)k.b * p.ns + ts / SC) * NP;
+  float* yb = p.y + ((int64_t)k.b * p.L + k.t0) * p.Dm + k.d;
 #pragma unroll
-      for (int n = 0; n < NP; ++n) p.hs[(sb + n) * p.Dm + k.d] = h[n];
-    }
+  for (int j = 0; j < kSsmChunk; ++j) {
+    const int t = k.t0 + j;
+    if (t < k.t1) {
+      if (j % kSsmSub == 0 && p.hs) {
+        const int64_t sb = ((int64_t)k.b * p.ns + t / kSsmSub) * NP;
 #pragma unroll
-    for (int j = 0; j < SC; ++j) {
-      const int t = ts + j;
-      if (t < k.t1) {
-        const int64_t xi = ((int64_t)k.b * p.L + t) * p.Dm + k.d;
-        const float dt = p.delta[xi], xv = p.x[xi], dx = dt * xv;
-        const float* Bt = p.B + ((int64_t)k.b * p.L + t) * p.N;
-        const float* Ct = p.C + ((int64_t)k.b * p.L + t) * p.N;
-        float y = 0.f;
-#pragma unroll
-        for (int n = 0; n < NP; ++n) {
-          h[n] = __builtin_fmaf(fexp2(dt * al[n]), h[n], dx * row_val(Bt, n, p.N));
-          y = __builtin_fmaf(row_val(Ct, n, p.N), h[n], y);
-        }
-        p.y[xi] = __builtin_fmaf(Dd, xv, y);
+        for (int n = 0; n < NP; ++n) p.hs[(sb + n) * p.Dm + k.d] = h[n];
       }
+      const float dt = dr[j], dx = dt * xr[j];
+      float y = 0.f;
+#pragma unroll
+      for (int n = 0; n < NP; ++n) {
+        h[n] = __builtin_fmaf(fexp2(dt * al[n]), h[n], dx * sB[j][n]);
+        y = __builtin_fmaf(sC[j][n], h[n], y);
+      }
+      yb[(int64_t)j * p.Dm] = __builtin_fmaf(Dd, xr[j], y);
     }
   }
 }
@@ -165,21 +195,28 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_fwd_out_kernel(const SsmParams 
 // sum(delta).
 template <int NP>
 __global__ __launch_bounds__(kSsmBlock) void ssm_bwd_local_kernel(const SsmParams p) {
+  __shared__ float sC[kSsmChunk][NP];
   const SsmBlock k = ssm_block(p);
+  stage_rows<NP>(p, k, p.C, sC);
+  __syncthreads();
   if (k.d >= p.Dm) return;
+  float dr[kSsmChunk], gr[kSsmChunk];
+  load_chunk(p, k, k.d, p.delta, dr);
+  load_chunk(p, k, k.d, p.dy, gr);
   float al[NP], gh[NP];
   load_al<NP>(p, k.d, true, al);
 #pragma unroll
   for (int n = 0; n < NP; ++n) gh[n] = 0.f;
   float sdt = 0.f;
-  for (int t = k.t1 - 1; t >= k.t0; --t) {
-    const int64_t xi = ((int64_t)k.b * p.L + t) * p.Dm + k.d;
-    const float dt = p.delta[xi], dyv = p.dy[xi];
-    const float* Ct = p.C + ((int64_t)k.b * p.L + t) * p.N;
 #pragma unroll
-    for (int n = 0; n < NP; ++n)
-      gh[n] = fexp2(dt * al[n]) * __builtin_fmaf(row_val(Ct, n, p.N), dyv, gh[n]);
-    sdt += dt;
+  for (int j = kSsmChunk - 1; j >= 0; --j) {
+    if (k.t0 + j < k.t1) {
+      const float dt = dr[j], dyv = gr[j];
+#pragma unroll
+      for (int n = 0; n < NP; ++n)
+        gh[n] = fexp2(dt * al[n]) * __builtin_fmaf(sC[j][n], dyv, gh[n]);
+      sdt += dt;
+    }
   }
   const int64_t cb = ((int64_t)k.b * p.nc + k.c) * NP;
 #pragma unroll
@@ -187,13 +224,17 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_bwd_local_kernel(const SsmParam
   p.sdt[((int64_t)k.b * p.nc + k.c) * p.Dm + k.d] = sdt;
 }
 
-// Sums v[0..V) over the 64 lanes of a wave.  log2(V) halving exchanges
-// leave each lane one value index, lane >> (6 - log2(V)), summed over the
-// lanes that share the lane's top log2(V) bits; the remaining exchanges
-// complete the 64-lane sum.  V - 1 + 6 - log2(V) shuffles in all.
-template <int V>
+// Sums v[0..V) over the lanes of a wave that share lane % LPC (the lanes
+// of one state group, one per channel).  log2(V) halving exchanges (masks
+// 32 down to 2^SH, SH = 6 - log2(V)) leave each lane one value index,
+// lane >> SH, summed over the lanes that share the lane's top log2(V) bits;
+// exchanges over the remaining channel bits (masks 2^(SH-1) down to LPC)
+// complete the sum.  The result is in the lanes whose bits between LPC and
+// 2^SH are zero.
+template <int V, int LPC>
 __device__ __forceinline__ float wave_sum_scatter(float (&v)[V], int lane) {
-  static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V: power of two <= 64");
+  static_assert(V >= 1 && V <= 32 && (V & (V - 1)) == 0, "V: power of two <= 32");
+  static_assert(V * LPC < 64, "state groups must leave channel bits to reduce");
 #pragma unroll
   for (int half = V / 2, m = 32; half >= 1; half /= 2, m /= 2) {
     const bool up = lane & m;
@@ -209,119 +250,111 @@ __device__ __forceinline__ float wave_sum_scatter(float (&v)[V], int lane) {
   }
   float s = v[0];
 #pragma unroll
-  for (int m = 32 / V; m >= 1; m /= 2) s += __shfl_xor(s, m, 64);
+  for (int m = 32 / V; m >= LPC; m /= 2) s += __shfl_xor(s, m, 64);
   return s;
 }
 
-// (6) Backward pass over one chunk, sub-chunk by sub-chunk from the last.
-// A sub-chunk's SC states are rebuilt from its saved entering state in parts
-// of HS steps (registers hold HS + 1 states of NP), the last part first; a
-// part q first advances the saved state over the q * HS steps before it.
-template <int NP, int HS>
+// (6) Backward pass over one chunk, sub-chunk by sub-chunk from the last:
+// the sub-chunk's 8 states are rebuilt in registers from its saved entering
+// state, then walked in reverse.  LPC lanes share a channel, each with NPL
+// of its states (NP = NPL * LPC), which keeps the 9 x NPL history in
+// registers; dx and ddelta are summed over the LPC lanes.
+template <int NPL, int LPC>
 __global__ __launch_bounds__(kSsmBlock) void ssm_bwd_chunk_kernel(const SsmParams p) {
+  constexpr int NP = NPL * LPC;
   constexpr int SC = kSsmSub;
-  constexpr int SH = 6 - __builtin_ctz(NP);
-  static_assert(SC % HS == 0, "HS must divide the sub-chunk");
+  constexpr int SH = 6 - __builtin_ctz(NPL);
   __shared__ float red[kSsmChunk][kWaves][2 * NP];
   __shared__ float sB[kSsmChunk][NP], sC[kSsmChunk][NP];  // the chunk's B, C rows
-  const SsmBlock k = ssm_block(p);
+  const SsmBlock k = ssm_block(p, p.ndblk_b, LPC);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int sub = tid & (LPC - 1), n0 = sub * NPL;
   const bool ok = k.d < p.Dm;  // idle lanes still take part in the sums, with zeros
   const int d = ok ? k.d : p.Dm - 1;
-  for (int e = tid; e < kSsmChunk * NP; e += kSsmBlock) {
-    const int j = e / NP, n = e % NP, t = k.t0 + j;
-    const bool in = t < k.t1 && n < p.N;
-    const int64_t bi = ((int64_t)k.b * p.L + t) * p.N + n;
-    sB[j][n] = in ? p.B[bi] : 0.f;
-    sC[j][n] = in ? p.C[bi] : 0.f;
-  }
+  const bool head = (lane & ((1 << SH) - 1) & ~(LPC - 1)) == 0;
+  stage_rows<NP>(p, k, p.B, sB);
+  stage_rows<NP>(p, k, p.C, sC);
   __syncthreads();
-  float al[NP], gh[NP], dA[NP];
-  load_al<NP>(p, d, ok, al);
-  const int64_t cb = ((int64_t)k.b * p.nc + k.c) * NP;
+  float al[NPL], gh[NPL], dA[NPL];
 #pragma unroll
-  for (int n = 0; n < NP; ++n) {
-    gh[n] = ok ? p.gc[(cb + n) * p.Dm + d] : 0.f;
-    dA[n] = 0.f;
+  for (int i = 0; i < NPL; ++i)
+    al[i] = (ok && n0 + i < p.N) ? p.A[(int64_t)d * p.N + n0 + i] * kLog2e : 0.f;
+  const int64_t cb = ((int64_t)k.b * p.nc + k.c) * NP + n0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    gh[i] = ok ? p.gc[(cb + i) * p.Dm + d] : 0.f;
+    dA[i] = 0.f;
   }
-  const float Dd = (ok && p.D) ? p.D[d] : 0.f;
+  const float Dd = (ok && p.D && sub == 0) ? p.D[d] : 0.f;  // skip term once per channel
   float dD = 0.f;
   const int nsub = (k.t1 - k.t0 + SC - 1) / SC;
   for (int s = nsub - 1; s >= 0; --s) {
     const int ts = k.t0 + s * SC;
-    const int64_t sb = ((int64_t)k.b * p.ns + ts / SC) * NP;
-    for (int q = SC / HS - 1; q >= 0; --q) {
-      const int tq = ts + q * HS;
-      if (tq >= k.t1) continue;  // uniform over the block
-      // hist[j]: the state entering step tq + j (hist[HS]: after the last).
-      float hist[HS + 1][NP];
+    // hist[j]: the state entering step ts + j (hist[SC]: after the last).
+    float hist[SC + 1][NPL];
+    const int64_t sb = ((int64_t)k.b * p.ns + ts / SC) * NP + n0;
 #pragma unroll
-      for (int n = 0; n < NP; ++n) hist[0][n] = ok ? p.hs[(sb + n) * p.Dm + d] : 0.f;
-      for (int t = ts; t < tq; ++t) {
+    for (int i = 0; i < NPL; ++i) hist[0][i] = ok ? p.hs[(sb + i) * p.Dm + d] : 0.f;
+#pragma unroll
+    for (int j = 0; j < SC; ++j) {
+      const int t = min(ts + j, k.t1 - 1);  // states past the end are never read
+      const int64_t xi = ((int64_t)k.b * p.L + t) * p.Dm + d;
+      const float dt = p.delta[xi], dx = dt * p.x[xi];
+      const float* Bt = sB[t - k.t0] + n0;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i)
+        hist[j + 1][i] = __builtin_fmaf(fexp2(dt * al[i]), hist[j][i], dx * Bt[i]);
+    }
+#pragma unroll
+    for (int j = SC - 1; j >= 0; --j) {
+      const int t = ts + j;
+      if (t < k.t1) {  // uniform over the block
         const int64_t xi = ((int64_t)k.b * p.L + t) * p.Dm + d;
-        const float dt = p.delta[xi], dx = dt * p.x[xi];
-        const float* Bt = sB[t - k.t0];
+        const float dt = p.delta[xi], xv = p.x[xi], dyv = ok ? p.dy[xi] : 0.f;
+        const float dtx = dt * xv;
+        const float* Bt = sB[t - k.t0] + n0;
+        const float* Ct = sC[t - k.t0] + n0;
+        float dx = Dd * dyv, ddt = 0.f;
+        float v[NPL];
+        // Recompute a here rather than keep the rebuild's values live.
+        float dto = dt;
+        asm volatile("" : "+v"(dto));
 #pragma unroll
-        for (int n = 0; n < NP; ++n)
-          hist[0][n] = __builtin_fmaf(fexp2(dt * al[n]), hist[0][n], dx * Bt[n]);
-      }
-#pragma unroll
-      for (int j = 0; j < HS; ++j) {
-        const int t = min(tq + j, k.t1 - 1);  // states past the end are never read
-        const int64_t xi = ((int64_t)k.b * p.L + t) * p.Dm + d;
-        const float dt = p.delta[xi], dx = dt * p.x[xi];
-        const float* Bt = sB[t - k.t0];
-#pragma unroll
-        for (int n = 0; n < NP; ++n)
-          hist[j + 1][n] = __builtin_fmaf(fexp2(dt * al[n]), hist[j][n], dx * Bt[n]);
-      }
-#pragma unroll
-      for (int j = HS - 1; j >= 0; --j) {
-        const int t = tq + j;
-        if (t < k.t1) {  // uniform over the block
-          const int64_t xi = ((int64_t)k.b * p.L + t) * p.Dm + d;
-          const float dt = p.delta[xi], xv = p.x[xi], dyv = ok ? p.dy[xi] : 0.f;
-          const float dtx = dt * xv;
-          const float* Bt = sB[t - k.t0];
-          const float* Ct = sC[t - k.t0];
-          float dx = Dd * dyv, ddt = 0.f;
-          float v[NP];
-          // Recompute a here rather than keep the rebuild's HS x NP values live.
-          float dto = dt;
-          asm volatile("" : "+v"(dto));
-#pragma unroll
-          for (int n = 0; n < NP; ++n) {
-            const float bn = Bt[n], cn = Ct[n];
-            const float a = fexp2(dto * al[n]);
-            const float ah = a * hist[j][n];
-            const float g = __builtin_fmaf(cn, dyv, gh[n]);
-            dx = __builtin_fmaf(g * dt, bn, dx);
-            ddt = __builtin_fmaf(g, __builtin_fmaf(bn, xv, al[n] * kLn2 * ah), ddt);
-            dA[n] = __builtin_fmaf(g * dt, ah, dA[n]);
-            v[n] = g * dtx;  // dB_t
-            gh[n] = a * g;
-          }
-          dD = __builtin_fmaf(dyv, xv, dD);
-          if (ok) {
-            p.dx[xi] = dx;
-            p.ddelta[xi] = ddt;
-          }
-          const bool head = (lane & ((1 << SH) - 1)) == 0;
-          float r = wave_sum_scatter<NP>(v, lane);
-          if (head) red[t - k.t0][wave][lane >> SH] = r;
-#pragma unroll
-          for (int n = 0; n < NP; ++n) v[n] = dyv * hist[j + 1][n];  // dC_t
-          r = wave_sum_scatter<NP>(v, lane);
-          if (head) red[t - k.t0][wave][NP + (lane >> SH)] = r;
+        for (int i = 0; i < NPL; ++i) {
+          const float bn = Bt[i], cn = Ct[i];
+          const float a = fexp2(dto * al[i]);
+          const float ah = a * hist[j][i];
+          const float g = __builtin_fmaf(cn, dyv, gh[i]);
+          dx = __builtin_fmaf(g * dt, bn, dx);
+          ddt = __builtin_fmaf(g, __builtin_fmaf(bn, xv, al[i] * kLn2 * ah), ddt);
+          dA[i] = __builtin_fmaf(g * dt, ah, dA[i]);
+          v[i] = g * dtx;  // dB_t
+          gh[i] = a * g;
         }
+#pragma unroll
+        for (int m = 1; m < LPC; m *= 2) {
+          dx += __shfl_xor(dx, m, 64);
+          ddt += __shfl_xor(ddt, m, 64);
+        }
+        dD = __builtin_fmaf(dyv, xv, dD);
+        if (ok && sub == 0) {
+          p.dx[xi] = dx;
+          p.ddelta[xi] = ddt;
+        }
+        float r = wave_sum_scatter<NPL, LPC>(v, lane);
+        if (head) red[t - k.t0][wave][n0 + (lane >> SH)] = r;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) v[i] = dyv * hist[j + 1][i];  // dC_t
+        r = wave_sum_scatter<NPL, LPC>(v, lane);
+        if (head) red[t - k.t0][wave][NP + n0 + (lane >> SH)] = r;
       }
     }
   }
   if (ok) {
-    // The chunk's adjoint slot is this lane's own: reuse it for the dA partials.
+    // The chunk's adjoint slots are this lane's own: reuse them for the dA partials.
 #pragma unroll
-    for (int n = 0; n < NP; ++n) p.gc[(cb + n) * p.Dm + d] = dA[n];
-    p.dDpart[((int64_t)k.b * p.nc + k.c) * p.Dm + d] = dD;
+    for (int i = 0; i < NPL; ++i) p.gc[(cb + i) * p.Dm + d] = dA[i];
+    if (sub == 0) p.dDpart[((int64_t)k.b * p.nc + k.c) * p.Dm + d] = dD;
   }
   __syncthreads();
   constexpr int V = 2 * NP;
@@ -372,7 +405,7 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_reduce_dbc_kernel(const SsmPara
   const int64_t per_blk = p.nb * p.L * V;
   if (i >= per_blk) return;
   float s = 0.f;
-  for (int blk = 0; blk < p.ndblk; ++blk) s += p.dBCpart[(int64_t)blk * per_blk + i];
+  for (int blk = 0; blk < p.ndblk_b; ++blk) s += p.dBCpart[(int64_t)blk * per_blk + i];
   const int q = (int)(i % V), n = q % NP;
   if (n < p.N) (q < NP ? p.dB : p.dC)[(i / V) * p.N + n] = s;
 }
@@ -381,8 +414,9 @@ unsigned blocks_for(int64_t n) { return (unsigned)((n + kSsmBlock - 1) / kSsmBlo
 
 template <int NP>
 void launch_ssm_t(const SsmParams& p, bool bwd, hipStream_t stream) {
-  constexpr int HS = NP > 8 ? 2 : 8;  // register budget: 2 waves per SIMD at NP = 16
+  constexpr int NPL = NP > 8 ? 8 : NP, LPC = NP / NPL;
   const dim3 grid((unsigned)(p.ndblk * p.nc * p.nb)), block(kSsmBlock);
+  const dim3 grid_b((unsigned)(p.ndblk_b * p.nc * p.nb));
   const dim3 cgrid(blocks_for(p.nb * NP * p.Dm));
   if (!bwd) {
     hipLaunchKernelGGL((ssm_fwd_local_kernel<NP>), grid, block, 0, stream, p);
@@ -391,7 +425,7 @@ void launch_ssm_t(const SsmParams& p, bool bwd, hipStream_t stream) {
   } else {
     hipLaunchKernelGGL((ssm_bwd_local_kernel<NP>), grid, block, 0, stream, p);
     hipLaunchKernelGGL((ssm_carry_kernel<true>), cgrid, block, 0, stream, p, NP, p.gc);
-    hipLaunchKernelGGL((ssm_bwd_chunk_kernel<NP, HS>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((ssm_bwd_chunk_kernel<NPL, LPC>), grid_b, block, 0, stream, p);
     const int64_t ncol = (int64_t)(NP + 1) * p.Dm;
     hipLaunchKernelGGL(ssm_reduce_dad_kernel, dim3((unsigned)((ncol + 63) / 64)), block, 0,
                        stream, p, NP);
@@ -403,6 +437,8 @@ void launch_ssm_t(const SsmParams& p, bool bwd, hipStream_t stream) {
 }  // namespace
 
 int ssm_padded_states(int N) { return N <= 4 ? 4 : N <= 8 ? 8 : N <= 16 ? 16 : 32; }
+
+int ssm_lanes_per_channel(int NP) { return NP > 8 ? NP / 8 : 1; }
 
 void launch_ssm(const SsmParams& p, bool bwd, hipStream_t stream) {
   switch (ssm_padded_states(p.N)) {
