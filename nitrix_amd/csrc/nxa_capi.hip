@@ -362,7 +362,7 @@ constexpr int kSsmMaxStates = 32;
 
 struct SsmLayout {
   int NP, nc, ns, ndblk, ndblk_b;
-  size_t hc, sdt, gc, dD, dBC;  // byte sizes of the workspace parts
+  size_t hc, sdt, gc, dD, dBC, dad;  // byte sizes of the workspace parts
   size_t state;                 // byte size of the saved sub-chunk states
 };
 
@@ -380,6 +380,7 @@ SsmLayout ssm_layout(int64_t nb, int32_t L, int32_t Dm, int32_t N) {
   s.sdt = align256((size_t)nb * s.nc * Dm * f);
   s.dD = s.sdt;
   s.dBC = align256((size_t)s.ndblk_b * nb * L * 2 * s.NP * f);
+  s.dad = align256((size_t)nxa::kSsmDadGroups * (s.NP + 1) * Dm * f);
   s.state = (size_t)nb * s.ns * s.NP * Dm * f;
   return s;
 }
@@ -585,7 +586,7 @@ size_t nxa_ssm_state_bytes(int64_t nb, int32_t L, int32_t d, int32_t n) {
 size_t nxa_ssm_workspace_bytes(int64_t nb, int32_t L, int32_t d, int32_t n, int is_bwd) {
   if (check_ssm(nb, L, d, n)) return 0;
   const SsmLayout s = ssm_layout(nb, L, d, n);
-  return is_bwd ? s.gc + s.sdt + s.dD + s.dBC : s.hc + s.sdt;
+  return is_bwd ? s.gc + s.sdt + s.dD + s.dBC + s.dad : s.hc + s.sdt;
 }
 
 int nxa_ssm_fwd(int64_t nb, int32_t L, int32_t d, int32_t n, const float* x,
@@ -640,7 +641,7 @@ int nxa_ssm_bwd(int64_t nb, int32_t L, int32_t d, int32_t n, const float* x,
   if ((D && !aligned(D, 4)) || (dD && !aligned(dD, 4)))
     return fail(NXA_E_LAYOUT, "selective scan: D / dD not 4-byte aligned");
   const SsmLayout s = ssm_layout(nb, L, d, n);
-  const size_t need = s.gc + s.sdt + s.dD + s.dBC;
+  const size_t need = s.gc + s.sdt + s.dD + s.dBC + s.dad;
   if (workspace_bytes < need || !aligned(workspace, 256))
     return fail(NXA_E_WORKSPACE, "selective scan: workspace needs %zu bytes, 256-byte aligned",
                 need);
@@ -664,6 +665,7 @@ int nxa_ssm_bwd(int64_t nb, int32_t L, int32_t d, int32_t n, const float* x,
   p.sdt = reinterpret_cast<float*>(ws + s.gc);
   p.dDpart = reinterpret_cast<float*>(ws + s.gc + s.sdt);
   p.dBCpart = reinterpret_cast<float*>(ws + s.gc + s.sdt + s.dD);
+  p.dadpart = reinterpret_cast<float*>(ws + s.gc + s.sdt + s.dD + s.dBC);
   p.nb = nb;
   p.L = L;
   p.Dm = d;

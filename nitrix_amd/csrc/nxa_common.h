@@ -120,6 +120,7 @@ struct SsmParams {
   float* hs;      // [nb][ns][NP][Dm] state entering each sub-chunk (may be null in fwd)
   float* dDpart;  // [nb][nc][Dm]
   float* dBCpart; // [ndblk_b][nb][L][2 NP]
+  float* dadpart; // [groups][(NP + 1) Dm] first-level sums of dA / dD
   int64_t nb;
   int L, Dm, N;
   int nc, ns;     // chunks, sub-chunks

@@ -21,6 +21,7 @@ int ssm_padded_states(int N);
 int ssm_lanes_per_channel(int NP);
 constexpr int kSsmChunk = 32;   // steps per chunk of the selective scan
 constexpr int kSsmSub = 8;      // steps per saved sub-chunk state
+constexpr int kSsmDadGroups = 16;  // row groups of the dA / dD reduction
 constexpr int kSsmBlock = 256;  // channels per block of the selective scan
 void launch_ssm(const SsmParams& p, bool bwd, hipStream_t stream);
 void launch_dbias_reduce(const Params& p, void* out, const int64_t* out_str,

@@ -141,6 +141,7 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_carry_kernel(const SsmParams p,
   const int n = (int)(nd / p.Dm), d = (int)(nd % p.Dm);
   const float al = n < p.N ? p.A[(int64_t)d * p.N + n] * kLog2e : 0.f;
   float H = 0.f;
+#pragma unroll 8
   for (int k = 0; k < p.nc; ++k) {
     const int c = REV ? p.nc - 1 - k : k;
     const int64_t ci = (b * p.nc + c) * per_b + nd;
@@ -369,32 +370,44 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_bwd_chunk_kernel(const SsmParam
   }
 }
 
-// (7a) dA [Dm, N] and dD [Dm]: sums over the nb * nc chunk partials, 64
-// columns per block, four row groups combined through LDS in a fixed order.
+// (7a) dA [Dm, N] and dD [Dm]: sums over the nb * nc chunk partials in two
+// fixed-order levels.  Level 1: block (x, y) sums rows y, y + G, ... (G =
+// gridDim.y) of 64 columns, four row groups combined through LDS, into
+// part[y][col]; level 2 sums the G partials of each column.
 __global__ __launch_bounds__(kSsmBlock) void ssm_reduce_dad_kernel(const SsmParams p, int NP) {
   __shared__ float part[kWaves][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t col = (int64_t)blockIdx.x * 64 + lane;
   const int64_t na = (int64_t)NP * p.Dm, ncol = na + p.Dm;
-  const int64_t rows = p.nb * p.nc;
+  const int64_t rows = p.nb * p.nc, step = (int64_t)gridDim.y * kWaves;
   float s = 0.f;
   if (col < ncol) {
+    const int64_t r0 = (int64_t)blockIdx.y * kWaves + w;
     if (col < na) {
-      for (int64_t r = w; r < rows; r += kWaves) s += p.gc[r * na + col];
+      for (int64_t r = r0; r < rows; r += step) s += p.gc[r * na + col];
     } else {
-      for (int64_t r = w; r < rows; r += kWaves) s += p.dDpart[r * p.Dm + (col - na)];
+      for (int64_t r = r0; r < rows; r += step) s += p.dDpart[r * p.Dm + (col - na)];
     }
   }
   part[w][lane] = s;
   __syncthreads();
-  if (w == 0 && col < ncol) {
-    s = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
-    if (col < na) {
-      const int n = (int)(col / p.Dm), d = (int)(col % p.Dm);
-      if (n < p.N) p.dA[(int64_t)d * p.N + n] = s;
-    } else if (p.dD) {
-      p.dD[col - na] = s;
-    }
+  if (w == 0 && col < ncol)
+    p.dadpart[blockIdx.y * ncol + col] =
+        (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+}
+
+__global__ __launch_bounds__(kSsmBlock) void ssm_reduce_dad2_kernel(const SsmParams p, int NP,
+                                                                   int groups) {
+  const int64_t col = (int64_t)blockIdx.x * kSsmBlock + threadIdx.x;
+  const int64_t na = (int64_t)NP * p.Dm, ncol = na + p.Dm;
+  if (col >= ncol) return;
+  float s = 0.f;
+  for (int g = 0; g < groups; ++g) s += p.dadpart[g * ncol + col];
+  if (col < na) {
+    const int n = (int)(col / p.Dm), d = (int)(col % p.Dm);
+    if (n < p.N) p.dA[(int64_t)d * p.N + n] = s;
+  } else if (p.dD) {
+    p.dD[col - na] = s;
   }
 }
 
@@ -427,8 +440,10 @@ void launch_ssm_t(const SsmParams& p, bool bwd, hipStream_t stream) {
     hipLaunchKernelGGL((ssm_carry_kernel<true>), cgrid, block, 0, stream, p, NP, p.gc);
     hipLaunchKernelGGL((ssm_bwd_chunk_kernel<NPL, LPC>), grid_b, block, 0, stream, p);
     const int64_t ncol = (int64_t)(NP + 1) * p.Dm;
-    hipLaunchKernelGGL(ssm_reduce_dad_kernel, dim3((unsigned)((ncol + 63) / 64)), block, 0,
-                       stream, p, NP);
+    hipLaunchKernelGGL(ssm_reduce_dad_kernel, dim3((unsigned)((ncol + 63) / 64), kSsmDadGroups),
+                       block, 0, stream, p, NP);
+    hipLaunchKernelGGL(ssm_reduce_dad2_kernel, dim3(blocks_for(ncol)), block, 0, stream, p, NP,
+                       kSsmDadGroups);
     hipLaunchKernelGGL(ssm_reduce_dbc_kernel, dim3(blocks_for(p.nb * p.L * 2 * NP)), block, 0,
                        stream, p, NP);
   }

@@ -74,14 +74,16 @@ def test_state_and_workspace_sizes(lib):
     hc = a256(nb * nc * np_ * d * 4)
     sdt = a256(nb * nc * d * 4)
     dbc = a256(ndblk * nb * length * 2 * np_ * 4)
+    dad = a256(16 * (np_ + 1) * d * 4)  # 16 row groups of the dA / dD sums
     assert lib.nxa_ssm_workspace_bytes(nb, length, d, n, 0) == hc + sdt
-    assert lib.nxa_ssm_workspace_bytes(nb, length, d, n, 1) == hc + 2 * sdt + dbc
+    assert lib.nxa_ssm_workspace_bytes(nb, length, d, n, 1) == hc + 2 * sdt + dbc + dad
     assert lib.nxa_ssm_state_bytes(1, 64, 8, 40) == 0
     # 16 states: the backward chunk pass runs two lanes per channel, so its
     # dB / dC partials come from blocks of 128 channels
     hc16 = a256(nb * nc * 16 * d * 4)
     dbc16 = a256(3 * nb * length * 2 * 16 * 4)
-    assert lib.nxa_ssm_workspace_bytes(nb, length, d, 16, 1) == hc16 + 2 * sdt + dbc16
+    dad16 = a256(16 * 17 * d * 4)
+    assert lib.nxa_ssm_workspace_bytes(nb, length, d, 16, 1) == hc16 + 2 * sdt + dbc16 + dad16
 
 
 def test_no_state_trajectory_in_memory(lib):
