@@ -241,12 +241,23 @@ __device__ __forceinline__ float wave_sum_scatter(float (&v)[V], int lane) {
     const bool up = lane & m;
 #pragma unroll
     for (int i = 0; i < half; ++i) {
-      // Select values, not addresses (an address select becomes a dynamic
-      // register index).
-      const float lo = v[i], hi = v[i + half];
-      const float keep = up ? hi : lo;
-      const float send = up ? lo : hi;
-      v[i] = keep + __shfl_xor(send, m, 64);
+      if (m >= 16) {
+        // v_permlane{32,16}_swap exchanges the upper lanes of v[i] with the
+        // lower lanes of v[i + half] (partners lane ^ m): afterwards the
+        // lower lane holds both lower values of index i, the upper lane both
+        // values of index i + half, with no select.
+        const uint32_t lo = __float_as_uint(v[i]), hi = __float_as_uint(v[i + half]);
+        const auto r = m == 32 ? __builtin_amdgcn_permlane32_swap(lo, hi, false, false)
+                               : __builtin_amdgcn_permlane16_swap(lo, hi, false, false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+      } else {
+        // Select values, not addresses (an address select becomes a dynamic
+        // register index).
+        const float lo = v[i], hi = v[i + half];
+        const float keep = up ? hi : lo;
+        const float send = up ? lo : hi;
+        v[i] = keep + __shfl_xor(send, m, 64);
+      }
     }
   }
   float s = v[0];
