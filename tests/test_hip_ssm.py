@@ -218,3 +218,34 @@ def test_bench_shape_forward_and_vjp_identities():
     assert ed <= GRAD_TOL
     for k, (a, b) in checks.items():
         assert abs(a - b) <= 1e-4 * abs(b), (k, a, b)
+
+
+def test_inference_forward_matches_training_forward():
+    # Without gradients the forward keeps no sub-chunk states (state NULL);
+    # the output is the same bits.
+    arrs = _inputs((3,), 77, 200, 12, 61, True, 'softplus')
+    with torch.no_grad():
+        y0 = selective_scan_hip(*_gpu(arrs)).cpu().numpy()
+    y1 = selective_scan_hip(*_gpu(arrs, grad=True)).detach().cpu().numpy()
+    assert np.array_equal(y0, y1)
+
+
+@pytest.mark.parametrize('seed', range(6))
+def test_random_shapes(seed):
+    rng = np.random.RandomState(100 + seed)
+    lead = tuple(int(v) for v in rng.randint(1, 3, size=rng.randint(0, 3)))
+    length, d, n = int(rng.randint(1, 300)), int(rng.randint(1, 700)), int(rng.randint(1, 33))
+    with_d = bool(rng.randint(2))
+    regime = ('mamba', 'softplus')[seed % 2]
+    print(f'[case] ssm random lead={lead} L={length} d={d} n={n} D={with_d} {regime}',
+          flush=True)
+    arrs = _inputs(lead, length, d, n, 200 + seed, with_d, regime)
+    dy = rng.standard_normal(arrs[0].shape).astype(np.float32)
+    y, grads = _run(arrs, dy)
+    a64 = [None if a is None else a.astype(np.float64) for a in arrs]
+    assert relerr(y, S.selective_scan(*a64)) <= FWD_TOL
+    wg = S.selective_scan_vjp(*a64, dy.astype(np.float64))
+    for g, w in zip(grads, wg):
+        if w is not None:
+            assert relerr(g, w) <= GRAD_TOL
+
