@@ -393,8 +393,11 @@ int check_ssm(int64_t nb, int32_t L, int32_t Dm, int32_t N) {
     return fail(NXA_E_UNSUPPORTED, "selective scan: state dim n=%d exceeds %d", N,
                 kSsmMaxStates);
   const SsmLayout s = ssm_layout(nb, L, Dm, N);
+  // Grids: chunk passes ndblk * nc * nb blocks, carry nb * NP * Dm / 256,
+  // dB / dC reduction nb * L * 2 NP / 256; all below 2^31.
   if ((int64_t)s.ndblk_b * s.nc * nb >= ((int64_t)1 << 31) ||
-      nb * s.NP * (int64_t)Dm >= ((int64_t)1 << 38))
+      nb * s.NP * (int64_t)Dm >= ((int64_t)1 << 38) ||
+      nb * (int64_t)L * 2 * s.NP >= ((int64_t)1 << 38))
     return fail(NXA_E_SHAPE, "selective scan: nb=%lld L=%d d=%d exceed the grid",
                 (long long)nb, L, Dm);
   return NXA_OK;
