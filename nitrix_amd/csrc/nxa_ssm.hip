@@ -85,14 +85,18 @@ __device__ __forceinline__ void stage_rows(const SsmParams& p, const SsmBlock& k
   }
 }
 
-// The lane's values of a [nb, L, Dm] tensor over the chunk, all loads issued
-// at once (steps past the end are left unset and never read).
-__device__ __forceinline__ void load_chunk(const SsmParams& p, const SsmBlock& k, int d,
-                                           const float* src, float (&r)[kSsmChunk]) {
-  const float* base = src + ((int64_t)k.b * p.L + k.t0) * p.Dm + d;
+// The lane's values of a [nb, L, Dm] tensor over KP steps of the chunk from
+// step j0, all loads issued at once (steps past the end are left unset and
+// never read).
+constexpr int kSsmPart = 16;
+
+template <int KP>
+__device__ __forceinline__ void load_part(const SsmParams& p, const SsmBlock& k, int d, int j0,
+                                          const float* src, float (&r)[KP]) {
+  const float* base = src + ((int64_t)k.b * p.L + k.t0 + j0) * p.Dm + d;
 #pragma unroll
-  for (int j = 0; j < kSsmChunk; ++j)
-    if (k.t0 + j < k.t1) r[j] = base[(int64_t)j * p.Dm];
+  for (int j = 0; j < KP; ++j)
+    if (k.t0 + j0 + j < k.t1) r[j] = base[(int64_t)j * p.Dm];
 }
 
 // (1) Local forward scan of a chunk from zero: end state and sum(delta).
@@ -103,22 +107,25 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_fwd_local_kernel(const SsmParam
   stage_rows<NP>(p, k, p.B, sB);
   __syncthreads();
   if (k.d >= p.Dm) return;
-  float dr[kSsmChunk], xr[kSsmChunk];
-  load_chunk(p, k, k.d, p.delta, dr);
-  load_chunk(p, k, k.d, p.x, xr);
   float al[NP], h[NP];
   load_al<NP>(p, k.d, true, al);
 #pragma unroll
   for (int n = 0; n < NP; ++n) h[n] = 0.f;
   float sdt = 0.f;
+#pragma unroll 1
+  for (int j0 = 0; j0 < kSsmChunk; j0 += kSsmPart) {
+    float dr[kSsmPart], xr[kSsmPart];
+    load_part(p, k, k.d, j0, p.delta, dr);
+    load_part(p, k, k.d, j0, p.x, xr);
 #pragma unroll
-  for (int j = 0; j < kSsmChunk; ++j) {
-    if (k.t0 + j < k.t1) {
-      const float dt = dr[j], dx = dt * xr[j];
+    for (int j = 0; j < kSsmPart; ++j) {
+      if (k.t0 + j0 + j < k.t1) {
+        const float dt = dr[j], dx = dt * xr[j];
 #pragma unroll
-      for (int n = 0; n < NP; ++n)
-        h[n] = __builtin_fmaf(fexp2(dt * al[n]), h[n], dx * sB[j][n]);
-      sdt += dt;
+        for (int n = 0; n < NP; ++n)
+          h[n] = __builtin_fmaf(fexp2(dt * al[n]), h[n], dx * sB[j0 + j][n]);
+        sdt += dt;
+      }
     }
   }
   const int64_t cb = ((int64_t)k.b * p.nc + k.c) * NP;
@@ -161,9 +168,6 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_fwd_out_kernel(const SsmParams 
   stage_rows<NP>(p, k, p.C, sC);
   __syncthreads();
   if (k.d >= p.Dm) return;
-  float dr[kSsmChunk], xr[kSsmChunk];
-  load_chunk(p, k, k.d, p.delta, dr);
-  load_chunk(p, k, k.d, p.x, xr);
   float al[NP], h[NP];
   load_al<NP>(p, k.d, true, al);
   const int64_t cb = ((int64_t)k.b * p.nc + k.c) * NP;
@@ -171,23 +175,29 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_fwd_out_kernel(const SsmParams 
   for (int n = 0; n < NP; ++n) h[n] = p.hc[(cb + n) * p.Dm + k.d];
   const float Dd = p.D ? p.D[k.d] : 0.f;
   float* yb = p.y + ((int64_t)k.b * p.L + k.t0) * p.Dm + k.d;
+#pragma unroll 1
+  for (int j0 = 0; j0 < kSsmChunk; j0 += kSsmPart) {
+    float dr[kSsmPart], xr[kSsmPart];
+    load_part(p, k, k.d, j0, p.delta, dr);
+    load_part(p, k, k.d, j0, p.x, xr);
 #pragma unroll
-  for (int j = 0; j < kSsmChunk; ++j) {
-    const int t = k.t0 + j;
-    if (t < k.t1) {
-      if (j % kSsmSub == 0 && p.hs) {
-        const int64_t sb = ((int64_t)k.b * p.ns + t / kSsmSub) * NP;
+    for (int jj = 0; jj < kSsmPart; ++jj) {
+      const int j = j0 + jj, t = k.t0 + j;
+      if (t < k.t1) {
+        if (jj % kSsmSub == 0 && p.hs) {
+          const int64_t sb = ((int64_t)k.b * p.ns + t / kSsmSub) * NP;
 #pragma unroll
-        for (int n = 0; n < NP; ++n) p.hs[(sb + n) * p.Dm + k.d] = h[n];
+          for (int n = 0; n < NP; ++n) p.hs[(sb + n) * p.Dm + k.d] = h[n];
+        }
+        const float dt = dr[jj], dx = dt * xr[jj];
+        float y = 0.f;
+#pragma unroll
+        for (int n = 0; n < NP; ++n) {
+          h[n] = __builtin_fmaf(fexp2(dt * al[n]), h[n], dx * sB[j][n]);
+          y = __builtin_fmaf(sC[j][n], h[n], y);
+        }
+        yb[(int64_t)j * p.Dm] = __builtin_fmaf(Dd, xr[jj], y);
       }
-      const float dt = dr[j], dx = dt * xr[j];
-      float y = 0.f;
-#pragma unroll
-      for (int n = 0; n < NP; ++n) {
-        h[n] = __builtin_fmaf(fexp2(dt * al[n]), h[n], dx * sB[j][n]);
-        y = __builtin_fmaf(sC[j][n], h[n], y);
-      }
-      yb[(int64_t)j * p.Dm] = __builtin_fmaf(Dd, xr[j], y);
     }
   }
 }
@@ -201,22 +211,25 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_bwd_local_kernel(const SsmParam
   stage_rows<NP>(p, k, p.C, sC);
   __syncthreads();
   if (k.d >= p.Dm) return;
-  float dr[kSsmChunk], gr[kSsmChunk];
-  load_chunk(p, k, k.d, p.delta, dr);
-  load_chunk(p, k, k.d, p.dy, gr);
   float al[NP], gh[NP];
   load_al<NP>(p, k.d, true, al);
 #pragma unroll
   for (int n = 0; n < NP; ++n) gh[n] = 0.f;
   float sdt = 0.f;
+#pragma unroll 1
+  for (int j0 = kSsmChunk - kSsmPart; j0 >= 0; j0 -= kSsmPart) {
+    float dr[kSsmPart], gr[kSsmPart];
+    load_part(p, k, k.d, j0, p.delta, dr);
+    load_part(p, k, k.d, j0, p.dy, gr);
 #pragma unroll
-  for (int j = kSsmChunk - 1; j >= 0; --j) {
-    if (k.t0 + j < k.t1) {
-      const float dt = dr[j], dyv = gr[j];
+    for (int jj = kSsmPart - 1; jj >= 0; --jj) {
+      if (k.t0 + j0 + jj < k.t1) {
+        const float dt = dr[jj], dyv = gr[jj];
 #pragma unroll
-      for (int n = 0; n < NP; ++n)
-        gh[n] = fexp2(dt * al[n]) * __builtin_fmaf(sC[j][n], dyv, gh[n]);
-      sdt += dt;
+        for (int n = 0; n < NP; ++n)
+          gh[n] = fexp2(dt * al[n]) * __builtin_fmaf(sC[j0 + jj][n], dyv, gh[n]);
+        sdt += dt;
+      }
     }
   }
   const int64_t cb = ((int64_t)k.b * p.nc + k.c) * NP;
