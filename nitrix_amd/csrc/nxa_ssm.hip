@@ -339,7 +339,9 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_bwd_chunk_kernel(const SsmParam
         const float dtx = dt * xv;
         const float* Bt = sB[t - k.t0] + n0;
         const float* Ct = sC[t - k.t0] + n0;
-        float dx = Dd * dyv, ddt = 0.f;
+        // dx = D dy + delta sum g B and ddelta = x sum g B + ln2 sum g al a h,
+        // from the two sums sgb = sum g B and sga = sum g al a h.
+        float sgb = 0.f, sga = 0.f;
         float v[NPL];
         // Recompute a here rather than keep the rebuild's values live.
         float dto = dt;
@@ -350,17 +352,19 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_bwd_chunk_kernel(const SsmParam
           const float a = fexp2(dto * al[i]);
           const float ah = a * hist[j][i];
           const float g = __builtin_fmaf(cn, dyv, gh[i]);
-          dx = __builtin_fmaf(g * dt, bn, dx);
-          ddt = __builtin_fmaf(g, __builtin_fmaf(bn, xv, al[i] * kLn2 * ah), ddt);
+          sgb = __builtin_fmaf(g, bn, sgb);
+          sga = __builtin_fmaf(g * al[i], ah, sga);
           dA[i] = __builtin_fmaf(g * dt, ah, dA[i]);
           v[i] = g * dtx;  // dB_t
           gh[i] = a * g;
         }
 #pragma unroll
         for (int m = 1; m < LPC; m *= 2) {
-          dx += __shfl_xor(dx, m, 64);
-          ddt += __shfl_xor(ddt, m, 64);
+          sgb += __shfl_xor(sgb, m, 64);
+          sga += __shfl_xor(sga, m, 64);
         }
+        const float dx = __builtin_fmaf(dt, sgb, Dd * dyv);
+        const float ddt = __builtin_fmaf(xv, sgb, kLn2 * sga);
         dD = __builtin_fmaf(dyv, xv, dD);
         if (ok && sub == 0) {
           p.dx[xi] = dx;
