@@ -49,7 +49,12 @@
 extern "C" {
 #endif
 
-#define NXA_VERSION 3
+#define NXA_VERSION 4
+
+/* Flags of nxa_workspace_bytes. */
+#define NXA_WS_FWD 0   /* the forward                                        */
+#define NXA_WS_BWD 1   /* the backward                                       */
+#define NXA_WS_DBIAS 2 /* with NXA_WS_BWD: a backward that writes dbias      */
 
 typedef enum { NXA_BF16 = 0, NXA_F32 = 1, NXA_F16 = 2 } nxa_dtype;
 
@@ -64,6 +69,9 @@ enum {
   NXA_E_UNSUPPORTED = -7  /* valid request this build does not tile          */
 };
 
+/* Row strides (q_str[2], k_str[2], v_str[2], o_str[2], bias_str[2]): 64 rows
+ * plus 256 elements must span less than 2^32 bytes (NXA_E_LAYOUT otherwise);
+ * the kernels address a tile's rows with 32-bit offsets. */
 typedef struct {
   int32_t B, H, Lq, Lk, D;  /* head dim of q, k; D <= 256, D % 8 == 0 (bf16,
                                fp16) or % 4 (fp32)                            */
@@ -88,10 +96,17 @@ int nxa_version(void);
  * Replaces _check_tileable (attention.py:708-765). */
 int nxa_check(const nxa_desc* desc, int has_bias, int has_mask);
 
-/* Bytes of caller-provided device workspace that nxa_fwd (is_bwd = 0) or
- * nxa_bwd (is_bwd = 1) needs for this descriptor. */
+/* Bytes of caller-provided device workspace that nxa_fwd (flags NXA_WS_FWD)
+ * or nxa_bwd (NXA_WS_BWD, or NXA_WS_BWD | NXA_WS_DBIAS when dbias is
+ * requested) needs for this descriptor: the mask's tile map (one byte per
+ * 64 x 64 tile of the mask's own extent), two fp32 values per query row in
+ * the backward, and for dbias of a bias shared across batch or heads an fp32
+ * accumulator of the bias's own extent plus one chunk of per-(batch, head)
+ * partials (at most the larger of that accumulator and 256 KiB per query
+ * row).  A workspace sized for the backward also serves the forward.
+ * Returns 0 for an invalid descriptor or flags. */
 size_t nxa_workspace_bytes(const nxa_desc* desc, int has_bias, int has_mask,
-                           int is_bwd);
+                           int flags);
 
 /* Forward: o = softmax(scale * q k^T + bias, masked) v and its lse.
  * bias / mask may be NULL; lse may be NULL.  When mask is given, the first
@@ -104,9 +119,11 @@ int nxa_fwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
 /* Backward: dq, dk, dv (and dbias if non-NULL) of sum(dO * o).
  * dbias has the extent of bias (size 1 on the axes whose bias stride is 0)
  * with strides dbias_str (B, H, Lq; unit stride over Lk); broadcast axes are
- * summed, as the reference's _unbroadcast does.  `workspace` must hold
- * nxa_workspace_bytes(desc, .., 1) bytes; when tilemap_ready is nonzero its
- * leading bytes hold the tile map written by nxa_fwd for the same mask. */
+ * summed, as the reference's _unbroadcast does, in a fixed order.
+ * `workspace` must hold nxa_workspace_bytes(desc, .., NXA_WS_BWD, or
+ * NXA_WS_BWD | NXA_WS_DBIAS when dbias is non-NULL) bytes; when
+ * tilemap_ready is nonzero its leading bytes hold the tile map written by
+ * nxa_fwd for the same mask. */
 int nxa_bwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
             const void* bias, const uint8_t* mask, const void* o,
             const float* lse, const void* dout, void* dq, void* dk, void* dv,

@@ -18,6 +18,11 @@ NXA_BF16 = 0
 NXA_F32 = 1
 NXA_F16 = 2
 
+# nxa_workspace_bytes flags
+NXA_WS_FWD = 0
+NXA_WS_BWD = 1
+NXA_WS_DBIAS = 2
+
 NXA_OK = 0
 NXA_E_ARG = -1
 NXA_E_SHAPE = -2

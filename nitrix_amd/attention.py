@@ -27,6 +27,7 @@ import math
 from typing import Optional, Sequence
 
 import torch
+from torch.autograd.function import once_differentiable
 
 from . import _lib
 from ._backend import (
@@ -106,6 +107,7 @@ class _RmsNormHip(torch.autograd.Function):
         return y.reshape(x.shape)
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, dy):
         x2, rstd = ctx.saved_tensors
         rows, d = x2.shape
@@ -241,10 +243,18 @@ def _check_tileable(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         raise HipNotTileable('q, k, v are on different devices.')
 
 
+def _row_stride_ok(stride: int, esize: int) -> bool:
+    """The kernels address up to 64 rows of a tile with 32-bit byte offsets
+    (``nxa_check`` rejects larger row strides with ``NXA_E_LAYOUT``)."""
+    return (64 * stride + 256) * esize < (1 << 32)
+
+
 def _layout_ok(x: torch.Tensor, epc: int) -> bool:
     if x.stride(-1) != 1 and x.shape[-1] != 1:
         return False
     if x.data_ptr() % 16 != 0:
+        return False
+    if not _row_stride_ok(x.stride(-2), x.element_size()):
         return False
     return all(s % epc == 0 for s in x.stride()[:-1])
 
@@ -263,7 +273,7 @@ def _as_bhst(
 ) -> torch.Tensor:
     h = lead[-1]
     y = x.expand(*lead, s, t).reshape(nb, h, s, t)
-    if y.stride(-1) != 1 and t != 1:
+    if (y.stride(-1) != 1 and t != 1) or not _row_stride_ok(y.stride(-2), y.element_size()):
         y = y.contiguous()
     return y
 
@@ -348,13 +358,14 @@ class _Prepared:
     def stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
 
-    def workspace_bytes(self, is_bwd: int) -> int:
+    def workspace_bytes(self, flags: int) -> int:
+        """``nxa_workspace_bytes`` for ``flags`` (``NXA_WS_*``)."""
         return _lib.lib().nxa_workspace_bytes(
-            ctypes.byref(self.desc), self.has_bias, self.has_mask, is_bwd
+            ctypes.byref(self.desc), self.has_bias, self.has_mask, flags
         )
 
-    def workspace(self, is_bwd: int) -> Optional[torch.Tensor]:
-        nbytes = self.workspace_bytes(is_bwd)
+    def workspace(self, flags: int) -> Optional[torch.Tensor]:
+        nbytes = self.workspace_bytes(flags)
         if nbytes == 0:
             return None
         return torch.empty(nbytes, dtype=torch.uint8, device=self.device)
@@ -363,8 +374,10 @@ class _Prepared:
 def _forward(prep: _Prepared, for_bwd: bool = False):
     """Run ``nxa_fwd``; returns ``(o [nb,h,s,d], lse [nb,h,s], workspace)``.
 
-    With ``for_bwd`` the workspace is sized for the backward as well (it
-    starts with the forward's tile map), so the backward reuses it as is."""
+    With ``for_bwd`` the workspace is sized for a backward without dbias (it
+    starts with the forward's tile map, then the per-row values), so such a
+    backward reuses it as is; a backward that wants dbias of a shared bias
+    allocates its larger workspace itself."""
     lib = _lib.lib()
     o = torch.empty(
         (prep.nb, prep.h, prep.s, prep.dv), dtype=prep.dtype, device=prep.device
@@ -372,7 +385,7 @@ def _forward(prep: _Prepared, for_bwd: bool = False):
     lse = torch.empty(
         (prep.nb, prep.h, prep.s), dtype=torch.float32, device=prep.device
     )
-    ws = prep.workspace(1 if for_bwd else 0)
+    ws = prep.workspace(_lib.NXA_WS_BWD if for_bwd else _lib.NXA_WS_FWD)
     _lib.check(
         lib.nxa_fwd(
             ctypes.byref(prep.desc),
@@ -431,15 +444,18 @@ def _backward(prep: _Prepared, o, lse, fwd_ws, dout, want_dbias: bool):
         )
         dbias_str = (ctypes.c_int64 * 3)(oh * lq * prep.t, lq * prep.t, prep.t)
     # The workspace begins with the forward's tile map; a forward workspace
-    # already sized for the backward is reused in place.
+    # already sized for this backward is reused in place.
+    flags = _lib.NXA_WS_BWD | (_lib.NXA_WS_DBIAS if dbias is not None else 0)
+    need = prep.workspace_bytes(flags)
     ready = 0
-    if fwd_ws is not None and fwd_ws.numel() >= prep.workspace_bytes(1):
+    if fwd_ws is not None and fwd_ws.numel() >= need:
         ws = fwd_ws
         ready = 1 if prep.mask is not None else 0
     else:
-        ws = prep.workspace(1)
+        ws = prep.workspace(flags)
         if prep.mask is not None and fwd_ws is not None:
-            ws[: fwd_ws.numel()].copy_(fwd_ws)
+            tm = prep.workspace_bytes(_lib.NXA_WS_FWD)
+            ws[:tm].copy_(fwd_ws[:tm])
             ready = 1
     _lib.check(
         lib.nxa_bwd(
@@ -471,21 +487,28 @@ class _SdpaHip(torch.autograd.Function):
 
     ``scale`` and ``causal`` are non-differentiable; the mask gets no
     gradient -- the structure of the reference's ``custom_vjp``
-    (``attention.py:661-700``)."""
+    (``attention.py:661-700``), whose residuals are the inputs, the output
+    and the log-sum-exp.  They are kept with ``save_for_backward``, so an
+    in-place change of an input between forward and backward raises
+    torch's version-counter error; the backward is not itself
+    differentiable (``once_differentiable``)."""
 
     @staticmethod
     def forward(ctx, q, k, v, bias, mask, scale, causal):
         prep = _Prepared(q, k, v, bias, mask, scale, causal)
         o, lse, ws = _forward(prep, for_bwd=any(ctx.needs_input_grad[:4]))
-        ctx.prep = prep
-        ctx.shapes = (tuple(q.shape), tuple(k.shape), tuple(v.shape))
-        ctx.save_for_backward(o, lse, ws if ws is not None else torch.empty(0))
+        ctx.args = (scale, causal)
+        ctx.save_for_backward(
+            q, k, v, bias, mask, o, lse, ws if ws is not None else torch.empty(0)
+        )
         return o.reshape(*prep.lead, prep.s, prep.dv)
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, dout):
-        o, lse, ws = ctx.saved_tensors
-        prep: _Prepared = ctx.prep
+        q, k, v, bias, mask, o, lse, ws = ctx.saved_tensors
+        ctx.shapes = (tuple(q.shape), tuple(k.shape), tuple(v.shape))
+        prep = _Prepared(q, k, v, bias, mask, *ctx.args)
         want_dbias = bool(ctx.needs_input_grad[3])
         dq, dk, dv, dbias_k = _backward(
             prep, o, lse, ws if ws.numel() else None, dout, want_dbias

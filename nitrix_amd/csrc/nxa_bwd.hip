@@ -142,8 +142,8 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) T Dt[DP * ST];
   __shared__ float lse_s[BQ], dlt_s[BQ];
 
-  const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nkt);
-  const int bh = vid / p.nkt;
+  const int vid = xcd_remap(blockIdx.x, p.nbh, p.nkt);
+  const int bh = p.bh0 + vid / p.nkt;
   const int kt = vid % p.nkt;
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -184,7 +184,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const Params p) {
   const uint8_t* mbase =
       p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] + kclamp
                  : nullptr;
-  const int64_t dbbase = b * p.dbias_str[0] + h * p.dbias_str[1] + key;
+  const int64_t dbbase = b * p.dbias_str[0] + h * p.dbias_str[1] + key - p.dbias_off;
   const bool full_db = DBIAS && p.dbias_mode == kDbiasFull;
 
   const int nq = (p.Lq + BQ - 1) / BQ;
@@ -447,29 +447,42 @@ __global__ __launch_bounds__(256) void dq_kernel(const Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// dbias reduction over broadcast batch / head axes (fp32 partials laid out
-// [B, H, LQ, Lk] -> out[OB, OH, LQ, Lk] in the bias dtype).  Deterministic:
-// each output element sums its partials in a fixed order.
+// dbias reduction over broadcast batch / head axes, one chunk of (batch, head)
+// pairs at a time.  The dK/dV launch of a chunk writes the fp32 partials of
+// its pairs bh0 .. bh0 + nbh - 1 as [nbh, LQ, Lk] (slot = pair - bh0); this
+// kernel adds them into the fp32 accumulator acc [OB, OH, LQ, Lk] (starting
+// from zero for the first chunk) and, for the last chunk, writes the sums to
+// `out` in the bias dtype.  Each output element adds its pairs in increasing
+// pair order whatever the chunk size, so the result is deterministic and
+// does not depend on the chunking.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void dbias_reduce_kernel(
-    const Params p, void* out, int64_t s0, int64_t s1, int64_t s2, int OB,
-    int OH, int LQ) {
-  const int64_t n = (int64_t)OB * OH * LQ * p.Lk;
+__global__ __launch_bounds__(256) void dbias_reduce_kernel(DbiasReduce r) {
+  const int64_t n = (int64_t)r.OB * r.OH * r.LQ * r.Lk;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
-  const int k = i % p.Lk;
-  int64_t t = i / p.Lk;
-  const int q = t % LQ;
-  t /= LQ;
-  const int oh = t % OH;
-  const int ob = t / OH;
-  const float* ws = reinterpret_cast<const float*>(p.dbias);
-  float acc = 0.f;
-  for (int b = (OB == 1 ? 0 : ob); b < (OB == 1 ? p.B : ob + 1); ++b)
-    for (int h = (OH == 1 ? 0 : oh); h < (OH == 1 ? p.H : oh + 1); ++h)
-      acc += ws[(((int64_t)b * p.H + h) * LQ + q) * p.Lk + k];
-  const int64_t off = ob * s0 + oh * s1 + q * s2 + k;
-  store_elem(p.bias_dtype, out, off, acc);
+  const int k = i % r.Lk;
+  int64_t t = i / r.Lk;
+  const int q = t % r.LQ;
+  t /= r.LQ;
+  const int oh = t % r.OH;
+  const int ob = t / r.OH;
+  const int bh1 = r.bh0 + r.nbh;
+  // Pairs (b, h) of this output: every b when the bias is shared over the
+  // batch (OB == 1), else b = ob; likewise for h.  Restricted to the chunk.
+  const int b_lo = max(r.OB == 1 ? 0 : ob, r.bh0 / r.H);
+  const int b_hi = min(r.OB == 1 ? r.B - 1 : ob, (bh1 - 1) / r.H);
+  float sum = r.first ? 0.f : r.acc[i];
+  const int64_t slot = (int64_t)r.LQ * r.Lk;
+  for (int b = b_lo; b <= b_hi; ++b) {
+    const int h_lo = max(r.OH == 1 ? 0 : oh, r.bh0 - b * r.H);
+    const int h_hi = min(r.OH == 1 ? r.H - 1 : oh, bh1 - 1 - b * r.H);
+    for (int h = h_lo; h <= h_hi; ++h)
+      sum += r.part[(int64_t)(b * r.H + h - r.bh0) * slot + (int64_t)q * r.Lk + k];
+  }
+  if (r.last)
+    store_elem(r.dtype, r.out, ob * r.s[0] + oh * r.s[1] + q * r.s[2] + k, sum);
+  else
+    r.acc[i] = sum;
 }
 
 // ---------------------------------------------------------------------------
@@ -489,7 +502,7 @@ void launch_delta(const Params& p, int io_dtype, hipStream_t stream) {
 template <typename T, int DP, int OUT, int CW = kColAll>
 static void launch_dkdv_t(Params p, hipStream_t stream) {
   p.nkt = (p.Lk + 127) / 128;
-  const int n = p.B * p.H * p.nkt;
+  const int n = p.nbh * p.nkt;
   hipLaunchKernelGGL((dkdv_kernel<T, DP, OUT, CW>), dim3(n), dim3(256), 0, stream, p);
 }
 
@@ -544,12 +557,10 @@ void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream) {
   }
 }
 
-void launch_dbias_reduce(const Params& p, void* out, const int64_t* out_str,
-                         int OB, int OH, int LQ, hipStream_t stream) {
-  const int64_t n = (int64_t)OB * OH * LQ * p.Lk;
+void launch_dbias_reduce(const DbiasReduce& r, hipStream_t stream) {
+  const int64_t n = (int64_t)r.OB * r.OH * r.LQ * r.Lk;
   const int nb = (int)((n + 255) / 256);
-  hipLaunchKernelGGL(dbias_reduce_kernel, dim3(nb), dim3(256), 0, stream, p,
-                     out, out_str[0], out_str[1], out_str[2], OB, OH, LQ);
+  hipLaunchKernelGGL(dbias_reduce_kernel, dim3(nb), dim3(256), 0, stream, r);
 }
 
 }  // namespace nxa

@@ -80,8 +80,8 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
   __shared__ uint8_t tcls[kMaxBwdTiles];
   __shared__ int sched_s[4];
 
-  const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nkt);
-  const int bh = vid / p.nkt;
+  const int vid = xcd_remap(blockIdx.x, p.nbh, p.nkt);
+  const int bh = p.bh0 + vid / p.nkt;
   const int kt = vid % p.nkt;
   const int b = bh / p.H, h = bh % p.H;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
   const float bkey = (HAS_BIAS && !bias_rows) ? load_bias1(p, bbase) * kLog2e : 0.f;
   const uint8_t* mbase =
       p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] + kc : nullptr;
-  const int64_t dbbase = b * p.dbias_str[0] + h * p.dbias_str[1] + key;
+  const int64_t dbbase = b * p.dbias_str[0] + h * p.dbias_str[1] + key - p.dbias_off;
   // Everything that depends on the key alone folds into one additive term
   // of the P wave's logits: the query-broadcast bias, -inf for a key past
   // Lk, and -inf for a key that a query-broadcast mask (key padding)
@@ -217,13 +217,16 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
   };
   auto tile_src = [&](int t) NXA_INLINE -> TileSrc {
     const int q0 = t < nq ? t * BQ : p.Lq;
-    const int left = p.Lq - q0;  // rows from q0 to the end (0: empty ranges)
+    // Rows of this tile that exist (0: empty ranges).  Each range covers
+    // only the tile's own rows, so its byte size stays below 64 row strides,
+    // which the host bounds below 2^32 bytes.
+    const int rows = min(p.Lq - q0, BQ);
     TileSrc s;
     s.q = make_rsrc(qp + (int64_t)q0 * qs,
-                    left > 0 ? (uint32_t)(((int64_t)(left - 1) * qs + p.D) * 2) : 0u);
+                    rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * qs + p.D) * 2) : 0u);
     s.d = make_rsrc(dop + (int64_t)q0 * os,
-                    left > 0 ? (uint32_t)(((int64_t)(left - 1) * os + p.Dv) * 2) : 0u);
-    s.r = make_rsrc((cw == 0 ? nlp : ndp) + q0, (uint32_t)max(left, 0) * 4u);
+                    rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * os + p.Dv) * 2) : 0u);
+    s.r = make_rsrc((cw == 0 ? nlp : ndp) + q0, (uint32_t)max(rows, 0) * 4u);
     return s;
   };
   // Copy j of a tile into stage st: j < NCPY the wave's share of Q, then of
@@ -695,14 +698,16 @@ __global__ __launch_bounds__(256, 2) void dq16_kernel(const Params p) {
   // tile issues the same copies).
   auto tile_src = [&](int i) NXA_INLINE -> TileSrc {
     const int k0 = i < n ? tile_of(i) * BN : p.Lk;
-    const int left = p.Lk - k0;
+    // Keys of this tile that exist (0: empty ranges); each range covers only
+    // the tile's own rows (below 64 row strides, bounded by the host).
+    const int rows = min(p.Lk - k0, BN);
     TileSrc s;
     s.k = make_rsrc(kp + (int64_t)k0 * ks,
-                    left > 0 ? (uint32_t)(((int64_t)(left - 1) * ks + p.D) * 2) : 0u);
+                    rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * ks + p.D) * 2) : 0u);
     s.v = make_rsrc(vp + (int64_t)k0 * vs,
-                    left > 0 ? (uint32_t)(((int64_t)(left - 1) * vs + p.Dv) * 2) : 0u);
+                    rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * vs + p.Dv) * 2) : 0u);
     if constexpr (ROW_BIAS)
-      s.r = make_rsrc(bp + k0, (uint32_t)max(left, 0) * 2u);
+      s.r = make_rsrc(bp + k0, (uint32_t)max(rows, 0) * 2u);
     return s;
   };
   // Copy j of a tile into stage st: K share, V share, then the bias row
@@ -914,7 +919,7 @@ __global__ __launch_bounds__(256, 2) void dq16_kernel(const Params p) {
 template <typename T, int DP, bool HB, bool CA, int DBM>
 static void launch_dkdv16_t(Params p, hipStream_t stream) {
   p.nkt = (p.Lk + 127) / 128;
-  const int n = p.B * p.H * p.nkt;
+  const int n = p.nbh * p.nkt;
   hipLaunchKernelGGL((dkdv16_kernel<T, DP, HB, CA, DBM>), dim3(n), dim3(512), 0,
                      stream, p);
 }

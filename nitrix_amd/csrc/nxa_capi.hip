@@ -86,6 +86,12 @@ int launch(const char* name, hipStream_t stream, F&& f) {
 // ---------------------------------------------------------------------------
 // Validation shared by every entry point.
 // ---------------------------------------------------------------------------
+// 64 rows of `stride` elements of `es` bytes, plus one more row of up to
+// 256 elements, span less than 2^32 bytes.
+bool row_stride_ok(int64_t stride, int es) {
+  return stride >= 0 && (64 * stride + 256) * es < ((int64_t)1 << 32);
+}
+
 int check_desc(const nxa_desc* d, int has_bias, int has_mask) {
   if (!d) return fail(NXA_E_ARG, "descriptor is NULL");
   if (!known_dtype(d->io_dtype))
@@ -123,10 +129,26 @@ int check_desc(const nxa_desc* d, int has_bias, int has_mask) {
                     "%s stride %d (%lld) must be a multiple of %d elements",
                     names[t], i, (long long)strs[t][i], epc);
     }
+  // The kernels address a tile's rows (at most 64) with 32-bit byte offsets
+  // from the tile's first row: 64 row strides (plus a row) must stay below
+  // 2^32 bytes.
+  const int io_es = esize(d->io_dtype);
+  const int64_t* rows_str[4] = {&d->q_str[2], &d->k_str[2], &d->v_str[2], &d->o_str[2]};
+  for (int t = 0; t < 4; ++t)
+    if (!row_stride_ok(*rows_str[t], io_es))
+      return fail(NXA_E_LAYOUT,
+                  "%s row stride %lld elements is too large: 64 rows must span "
+                  "less than 2^32 bytes",
+                  names[t], (long long)*rows_str[t]);
   if (has_bias)
     for (int i = 0; i < 3; ++i)
       if (d->bias_str[i] < 0)
         return fail(NXA_E_LAYOUT, "bias stride %d is negative", i);
+  if (has_bias && !row_stride_ok(d->bias_str[2], esize(d->bias_dtype)))
+    return fail(NXA_E_LAYOUT,
+                "bias row stride %lld elements is too large: 64 rows must span "
+                "less than 2^32 bytes",
+                (long long)d->bias_str[2]);
   if (has_mask)
     for (int i = 0; i < 3; ++i)
       if (d->mask_str[i] < 0)
@@ -160,9 +182,17 @@ struct DbiasGeom {
   int LQ;          // rows of dbias: Lq (full) or 1 (column sum)
   bool reduce;     // batch / head axes broadcast: fp32 partials + reduction
   int OB, OH;
-  size_t partial_bytes;
+  int chunk;       // (batch, head) pairs per dK/dV launch when reducing
+  size_t acc_bytes, partial_bytes;
 };
 
+// dbias over a bias shared across batch or heads is summed over those axes.
+// The dK/dV kernel writes fp32 partials per (batch, head) pair; the pairs
+// run in chunks, each followed by a reduction into an fp32 accumulator of the
+// bias's own extent, so the workspace is that accumulator plus one chunk of
+// partials -- not B * H * Lq * Lk.  A chunk holds as many pairs as the
+// accumulator has slots (so the partials never exceed it), or more when that
+// gives the dK/dV launch fewer than ~512 blocks (two per CU).
 DbiasGeom dbias_geom(const nxa_desc* d) {
   DbiasGeom g;
   const bool colsum = d->Lq > 1 && d->bias_str[2] == 0;
@@ -171,28 +201,40 @@ DbiasGeom dbias_geom(const nxa_desc* d) {
   g.OB = d->bias_str[0] == 0 ? 1 : d->B;
   g.OH = d->bias_str[1] == 0 ? 1 : d->H;
   g.reduce = (d->B > 1 && g.OB == 1) || (d->H > 1 && g.OH == 1);
-  g.partial_bytes =
-      g.reduce ? (size_t)d->B * d->H * g.LQ * (size_t)d->Lk * sizeof(float) : 0;
+  const int64_t pairs = (int64_t)d->B * d->H;
+  const int64_t nkt = (d->Lk + 127) / 128;
+  int64_t chunk = (512 + nkt - 1) / nkt;
+  if (chunk < (int64_t)g.OB * g.OH) chunk = (int64_t)g.OB * g.OH;
+  if (chunk > pairs) chunk = pairs;
+  g.chunk = (int)chunk;
+  const size_t slot = (size_t)g.LQ * (size_t)d->Lk * sizeof(float);
+  g.acc_bytes = g.reduce ? (size_t)g.OB * g.OH * slot : 0;
+  g.partial_bytes = g.reduce ? (size_t)chunk * slot : 0;
   return g;
 }
 
 struct WsLayout {
-  size_t tilemap, delta, partial, total;
+  size_t tilemap, delta, acc, partial, total;
 };
 
-WsLayout ws_layout(const nxa_desc* d, int has_bias, int has_mask, int is_bwd) {
-  WsLayout w{0, 0, 0, 0};
+// flags: NXA_WS_BWD (bit 0) sizes the backward's per-row values, and
+// NXA_WS_DBIAS (bit 1) its dbias reduction buffers.
+WsLayout ws_layout(const nxa_desc* d, int has_bias, int has_mask, int flags) {
+  WsLayout w{0, 0, 0, 0, 0};
   size_t off = 0;
   if (has_mask) {
     w.tilemap = off;
     off += align256(mask_geom(d).bytes);
   }
-  if (is_bwd) {
+  if (flags & NXA_WS_BWD) {
     w.delta = off;  // -delta[B*H*Lq], then -lse2[B*H*Lq]
     off += 2 * align256((size_t)d->B * d->H * d->Lq * sizeof(float));
-    if (has_bias) {
+    if (has_bias && (flags & NXA_WS_DBIAS)) {
+      const DbiasGeom g = dbias_geom(d);
+      w.acc = off;
+      off += align256(g.acc_bytes);
       w.partial = off;
-      off += align256(dbias_geom(d).partial_bytes);
+      off += align256(g.partial_bytes);
     }
   }
   w.total = off;
@@ -274,6 +316,8 @@ nxa::Params base_params(const nxa_desc* d, const void* q, const void* k,
   }
   p.B = d->B;
   p.H = d->H;
+  p.bh0 = 0;
+  p.nbh = d->B * d->H;
   p.Lq = d->Lq;
   p.Lk = d->Lk;
   p.D = d->D;
@@ -425,9 +469,13 @@ int nxa_check(const nxa_desc* desc, int has_bias, int has_mask) {
 }
 
 size_t nxa_workspace_bytes(const nxa_desc* desc, int has_bias, int has_mask,
-                           int is_bwd) {
+                           int flags) {
   if (check_desc(desc, has_bias, has_mask) != NXA_OK) return 0;
-  return ws_layout(desc, has_bias, has_mask, is_bwd).total;
+  if (flags & ~(NXA_WS_BWD | NXA_WS_DBIAS)) {
+    fail(NXA_E_ARG, "workspace flags %d: only NXA_WS_BWD | NXA_WS_DBIAS", flags);
+    return 0;
+  }
+  return ws_layout(desc, has_bias, has_mask, flags).total;
 }
 
 int nxa_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
@@ -478,7 +526,8 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
       return fail(NXA_E_UNSUPPORTED,
                   "backward needs q materialised over axis %d (stride 0)", i);
   }
-  const WsLayout ws = ws_layout(d, bias != nullptr, mask != nullptr, 1);
+  const WsLayout ws = ws_layout(d, bias != nullptr, mask != nullptr,
+                                NXA_WS_BWD | (dbias ? NXA_WS_DBIAS : 0));
   if (!workspace || workspace_bytes < ws.total)
     return fail(NXA_E_WORKSPACE, "backward needs %zu workspace bytes, got %zu",
                 ws.total, workspace ? workspace_bytes : (size_t)0);
@@ -510,6 +559,7 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
     dg = dbias_geom(d);
     p.dbias_mode = dg.mode;
     if (dg.reduce) {
+      // Partials of one chunk of pairs, slot = pair - bh0 (dbias_off).
       p.dbias = wsb + ws.partial;
       p.dbias_f32 = 1;
       p.dbias_str[0] = (int64_t)d->H * dg.LQ * d->Lk;
@@ -524,18 +574,43 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
   if (dq_first &&
       (rc = launch("dq", stream, [&] { nxa::launch_dq(p, d->io_dtype, dp, stream); })))
     return rc;
-  if ((rc = launch("dkdv", stream,
-                   [&] { nxa::launch_dkdv(p, d->io_dtype, dp, stream); })))
-    return rc;
+  if (!(dbias && dg.reduce)) {
+    if ((rc = launch("dkdv", stream,
+                     [&] { nxa::launch_dkdv(p, d->io_dtype, dp, stream); })))
+      return rc;
+  } else {
+    const int pairs = d->B * d->H;
+    nxa::DbiasReduce r{};
+    r.part = reinterpret_cast<const float*>(wsb + ws.partial);
+    r.acc = reinterpret_cast<float*>(wsb + ws.acc);
+    r.out = dbias;
+    for (int i = 0; i < 3; ++i) r.s[i] = dbias_str[i];
+    r.B = d->B;
+    r.H = d->H;
+    r.OB = dg.OB;
+    r.OH = dg.OH;
+    r.LQ = dg.LQ;
+    r.Lk = d->Lk;
+    r.dtype = d->bias_dtype;
+    for (int bh0 = 0; bh0 < pairs; bh0 += dg.chunk) {
+      p.bh0 = bh0;
+      p.nbh = pairs - bh0 < dg.chunk ? pairs - bh0 : dg.chunk;
+      p.dbias_off = (int64_t)bh0 * dg.LQ * d->Lk;
+      if ((rc = launch("dkdv", stream,
+                       [&] { nxa::launch_dkdv(p, d->io_dtype, dp, stream); })))
+        return rc;
+      r.bh0 = p.bh0;
+      r.nbh = p.nbh;
+      r.first = bh0 == 0;
+      r.last = bh0 + p.nbh == pairs;
+      if ((rc = launch("dbias_reduce", stream,
+                       [&] { nxa::launch_dbias_reduce(r, stream); })))
+        return rc;
+    }
+  }
   if (!dq_first &&
       (rc = launch("dq", stream, [&] { nxa::launch_dq(p, d->io_dtype, dp, stream); })))
     return rc;
-  if (dbias && dg.reduce) {
-    rc = launch("dbias_reduce", stream, [&] {
-      nxa::launch_dbias_reduce(p, dbias, dbias_str, dg.OB, dg.OH, dg.LQ, stream);
-    });
-    if (rc) return rc;
-  }
   return NXA_OK;
 }
 

@@ -82,6 +82,9 @@ struct Params {
   int Dv;              // head dim of v, o, dO, dv (D: q, k, dq, dk)
   int nqt;             // query tiles of the launching kernel (grid decode)
   int nkt;             // key tiles of the launching kernel
+  int bh0, nbh;        // dK/dV launches cover (batch, head) pairs bh0 .. bh0+nbh-1
+                       // (pair index b * H + h)
+  int64_t dbias_off;   // subtracted from every dbias offset (chunked partials)
   float scale;
   float scale_log2;    // scale * log2(e)
   int causal;

@@ -24,7 +24,17 @@ constexpr int kSsmSub = 8;      // steps per saved sub-chunk state
 constexpr int kSsmDadGroups = 16;  // row groups of the dA / dD reduction
 constexpr int kSsmBlock = 256;  // channels per block of the selective scan
 void launch_ssm(const SsmParams& p, bool bwd, hipStream_t stream);
-void launch_dbias_reduce(const Params& p, void* out, const int64_t* out_str,
-                         int OB, int OH, int LQ, hipStream_t stream);
+// One chunk of the dbias reduction over broadcast batch / head axes.
+struct DbiasReduce {
+  const float* part;  // [nbh, LQ, Lk] fp32 partials of pairs bh0 .. bh0 + nbh - 1
+  float* acc;         // [OB, OH, LQ, Lk] fp32 running sums
+  void* out;          // dbias [OB, OH, LQ, Lk] in `dtype`, strides s (unit over Lk)
+  int64_t s[3];
+  int B, H, OB, OH, LQ, Lk;
+  int bh0, nbh;
+  int first, last;    // first chunk: sums start at zero; last: write `out`
+  int dtype;
+};
+void launch_dbias_reduce(const DbiasReduce& r, hipStream_t stream);
 
 }  // namespace nxa

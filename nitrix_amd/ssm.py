@@ -28,6 +28,7 @@ import math
 from typing import Optional
 
 import torch
+from torch.autograd.function import once_differentiable
 
 from . import _lib
 from ._backend import (
@@ -308,7 +309,13 @@ def _scan_backward(prep: _ScanPrep, state: torch.Tensor, dy: torch.Tensor):
 
 
 class _ScanHip(torch.autograd.Function):
-    """Fused forward, recompute-adjoint fused backward."""
+    """Fused forward, recompute-adjoint fused backward.
+
+    The fp32 views the kernels read (which alias the caller's tensors when
+    those are already contiguous fp32) and the saved sub-chunk states are
+    kept with ``save_for_backward``, so an in-place change of an input
+    between forward and backward raises torch's version-counter error; the
+    backward is not itself differentiable."""
 
     @staticmethod
     def forward(ctx, x, delta, A, B, C, D):
@@ -316,14 +323,18 @@ class _ScanHip(torch.autograd.Function):
         keep = any(ctx.needs_input_grad)
         y, state = _scan_forward(prep, keep)
         if keep:
+            ctx.save_for_backward(prep.x, prep.delta, prep.A, prep.B, prep.C, prep.D, state)
+            for name in ('x', 'delta', 'A', 'B', 'C', 'D'):
+                setattr(prep, name, None)
             ctx.prep = prep
-            ctx.state = state
         return y.reshape(*prep.batch, prep.length, prep.d).to(prep.io)
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, dy):
         prep = ctx.prep
-        dx, ddelta, dA, dB, dC, dD = _scan_backward(prep, ctx.state, dy)
+        prep.x, prep.delta, prep.A, prep.B, prep.C, prep.D, state = ctx.saved_tensors
+        dx, ddelta, dA, dB, dC, dD = _scan_backward(prep, state, dy)
         lead = prep.batch
         out = []
         grads = (dx, ddelta, dA, dB, dC)

@@ -44,7 +44,7 @@ def test_header_declares_the_expected_api():
 def test_library_exports_every_declared_function(lib):
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.nxa_version() == 3
+    assert lib.nxa_version() == 4
 
 
 def _desc(B=2, H=3, Lq=100, Lk=70, D=64, dtype=_lib.NXA_BF16):
@@ -130,10 +130,67 @@ def test_workspace_layout(lib):
     assert lib.nxa_workspace_bytes(ctypes.byref(d), 0, 0, 1) == 2 * 256 * (
         (rows + 255) // 256
     )
-    # bias shared over the batch: fp32 dbias partials [B,H,Lq,Lk] are added
-    part = 2 * 3 * 100 * 70 * 4
-    got = lib.nxa_workspace_bytes(ctypes.byref(d), 1, 0, 1)
-    assert got == 2 * 256 * ((rows + 255) // 256) + 256 * ((part + 255) // 256)
+    # bias shared over the batch, no dbias wanted: nothing more
+    assert lib.nxa_workspace_bytes(ctypes.byref(d), 1, 0, _lib.NXA_WS_BWD) == 2 * 256 * (
+        (rows + 255) // 256
+    )
+    # with dbias: an fp32 accumulator of the bias extent [1,H,Lq,Lk] plus one
+    # chunk of per-(batch, head) partials; here every pair fits one chunk
+    slot = 100 * 70 * 4
+    acc = 3 * slot
+    part = min(2 * 3, max(3, -(-512 // 1))) * slot
+    got = lib.nxa_workspace_bytes(ctypes.byref(d), 1, 0, _lib.NXA_WS_BWD | _lib.NXA_WS_DBIAS)
+    assert got == 2 * 256 * ((rows + 255) // 256) + 256 * ((acc + 255) // 256) + 256 * (
+        (part + 255) // 256
+    )
+    # unknown flags are rejected
+    assert lib.nxa_workspace_bytes(ctypes.byref(d), 1, 0, 4) == 0
+
+
+def test_dbias_workspace_is_bounded_by_the_bias_extent(lib):
+    """A bias shared over many (batch, head) pairs: the dbias buffers are the
+    fp32 accumulator of the bias's own extent plus one chunk of partials
+    (enough pairs for ~512 dK/dV blocks), not B * H * Lq * Lk."""
+    B, H, L = 4096, 4, 343  # windowed attention: many windows share a bias
+    d = _desc(B=B, H=H, Lq=L, Lk=L, D=32)
+    d.bias_str[:] = (0, L * L, L)  # [1, H, L, L]
+    base = lib.nxa_workspace_bytes(ctypes.byref(d), 1, 0, _lib.NXA_WS_BWD)
+    got = lib.nxa_workspace_bytes(ctypes.byref(d), 1, 0, _lib.NXA_WS_BWD | _lib.NXA_WS_DBIAS)
+    slot = L * L * 4
+    nkt = -(-L // 128)
+    chunk = max(H, -(-512 // nkt))
+    assert got - base == 256 * (-(-H * slot // 256)) + 256 * (-(-chunk * slot // 256))
+    assert got - base < B * H * slot / 50
+    # a full (unshared) bias needs no dbias buffers at all
+    d.bias_str[:] = (H * L * L, L * L, L)
+    assert lib.nxa_workspace_bytes(ctypes.byref(d), 1, 0, _lib.NXA_WS_BWD | _lib.NXA_WS_DBIAS) == base
+
+
+@pytest.mark.parametrize('which', ['q', 'k', 'v', 'o'])
+def test_row_stride_bound(lib, which):
+    """64 rows of a tile are addressed with 32-bit byte offsets: a row stride
+    whose 64 rows reach 2^32 bytes is NXA_E_LAYOUT, one just below is fine."""
+    d = _desc()
+    limit = ((1 << 32) // 2 - 256) // 64  # bf16 elements; strides are multiples of 8
+    ok = (limit - 1) // 8 * 8
+    bad = -(-limit // 8) * 8
+    getattr(d, f'{which}_str')[2] = ok
+    assert _check(lib, d) == _lib.NXA_OK
+    getattr(d, f'{which}_str')[2] = bad
+    assert _check(lib, d) == _lib.NXA_E_LAYOUT
+    assert 'row stride' in lib.nxa_last_error().decode()
+
+
+def test_bias_row_stride_bound(lib):
+    d = _desc()
+    d.bias_dtype = _lib.NXA_F32
+    limit = ((1 << 32) // 4 - 256) // 64
+    d.bias_str[2] = limit - 1
+    assert _check(lib, d) == _lib.NXA_OK
+    d.bias_str[2] = limit + 1
+    assert _check(lib, d) == _lib.NXA_E_LAYOUT
+    assert 'bias row stride' in lib.nxa_last_error().decode()
+    assert _check(lib, d, has_bias=0) == _lib.NXA_OK  # ignored without a bias
 
 
 def test_entry_points_reject_null_buffers_without_a_gpu(lib):

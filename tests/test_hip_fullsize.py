@@ -1,12 +1,19 @@
 """Parity at the BASELINE configurations' full sizes (GPU only).
 
 The CPU oracle cannot hold these problems whole (8.6-34 GB of fp32 logits per
-tensor), so each configuration is checked two ways on the same seeded inputs:
+tensor), so each configuration is checked three ways on the same seeded
+inputs:
 
-* **sampled rows** -- the float64 oracle (``oracle/attention.py``) on a
-  handful of query rows of a few (batch, head) slices, with the full keys,
-  values, bias row and mask row of each: the output rows and the dQ rows are
-  exact functions of those rows alone (dQ_i = scale sum_j dS_ij k_j);
+* **one whole (batch, head) slice** -- out, dQ, dK, dV (and the bias
+  gradient of C5's query-broadcast bias) of every row and key of the slice,
+  elementwise against the float64 oracle computed in blocks of query rows
+  (``oracle.attention.sdpa_slice_chunked``, pinned on the CPU against the
+  whole-matrix oracle);
+* **sampled rows** -- the float64 oracle (``oracle/attention.py``) on whole
+  64-row tiles (start, middle, tail) of a few other (batch, head) slices,
+  with the full keys, values, bias row and mask row of each: the output rows
+  and the dQ rows are exact functions of those rows alone
+  (dQ_i = scale sum_j dS_ij k_j);
 * **size-independent identities** of the attention backward, exact in
   arithmetic for every row that keeps at least one key:
     - sum_j dS_ij = 0, hence sum_j dK_j = 0 and sum_j dbias_j = 0 (dbias
@@ -103,6 +110,35 @@ def _identities(dk, dv, dout, live_rows, *, dbias=None, dead_keys=None):
         assert torch.count_nonzero(dv[dead_keys]) == 0, 'masked key has dV != 0'
 
 
+def _tiles(L):
+    """Whole 64-row tiles at the start, the middle and the tail."""
+    mid = (L // 2) // 64 * 64
+    return list(range(0, 64)) + list(range(mid, mid + 64)) + list(range(L - 64, L))
+
+
+def _check_slice(q, k, v, dout, out, grads, b, h, *, scale, keep_rows=None,
+                 bias_rows=None, bias_key=None, causal=False, dbias_col=None,
+                 chunk=512):
+    """Every output (and gradient) of slice (b, h) against the chunked
+    float64 oracle.  ``grads`` = (dq, dk, dv) tensors or None."""
+    r = O.sdpa_slice_chunked(
+        _np(q[b, h]), _np(k[b, h]), _np(v[b, h]),
+        None if grads is None else _np(dout[b, h]),
+        scale=scale, keep_rows=keep_rows, bias_rows=bias_rows, bias_key=bias_key,
+        causal=causal, chunk=chunk)
+    checks = [('out', out)]
+    if grads is not None:
+        checks += [('dq', grads[0]), ('dk', grads[1]), ('dv', grads[2])]
+    for name, t in checks:
+        e = _relerr(_np(t[b, h]), r[name])
+        print(f'  slice ({b},{h}) {name} relerr {e:.2e}', flush=True)
+        assert e <= REL, f'slice ({b},{h}) {name} relerr {e:.3e}'
+    if dbias_col is not None:
+        e = _relerr(_np(dbias_col), r['dbias_col'])
+        print(f'  slice ({b},{h}) dbias relerr {e:.2e}', flush=True)
+        assert e <= REL, f'slice ({b},{h}) dbias relerr {e:.3e}'
+
+
 def _fwd_bwd(q, k, v, dout, **kw):
     from nitrix_amd import scaled_dot_product_attention
 
@@ -127,10 +163,13 @@ def test_c2_key_padding_b8_h16_l4096_d128():
             < torch.as_tensor(valid, device=_dev())[:, None])[:, None, None, :]
     out = _fwd_bwd(q, k, v, dout, mask=mask)
     scale = 1.0 / math.sqrt(D)
-    for b, h in ((0, 0), (6, 11), (2, 15)):
-        rows = [0, 1, 777, L - 1]
+    for b, h in ((0, 0), (2, 15)):
         mrow = np.arange(L) < valid[b]
-        _check_rows(q, k, v, dout, out, q.grad, b, h, rows, scale=scale, mask_row=mrow)
+        _check_rows(q, k, v, dout, out, q.grad, b, h, _tiles(L), scale=scale, mask_row=mrow)
+    b, h = 6, 11
+    mrow = np.arange(L) < valid[b]
+    _check_slice(q, k, v, dout, out, (q.grad, k.grad, v.grad), b, h, scale=scale,
+                 keep_rows=lambda r0, r1: np.broadcast_to(mrow, (r1 - r0, L)))
     dead = ~mask[:, 0, 0, :]  # [B, L]
     dead = dead[:, None, :].expand(B, H, L)
     _identities(k.grad, v.grad, dout, torch.ones(B, H, L, device=_dev(), dtype=torch.float64),
@@ -147,9 +186,9 @@ def test_c3_causal_b4_h32_l8192_d128():
     dout = _randn(gen, B, H, L, D)
     out = _fwd_bwd(q, k, v, dout, causal=True)
     scale = 1.0 / math.sqrt(D)
-    for b, h in ((0, 0), (3, 31)):
-        rows = [0, 63, 64, 4000, L - 1]
-        _check_rows(q, k, v, dout, out, q.grad, b, h, rows, scale=scale, causal=True)
+    _check_rows(q, k, v, dout, out, q.grad, 0, 0, _tiles(L), scale=scale, causal=True)
+    _check_slice(q, k, v, dout, out, (q.grad, k.grad, v.grad), 3, 31, scale=scale,
+                 causal=True)
     _identities(k.grad, v.grad, dout, torch.ones(B, H, L, device=_dev(), dtype=torch.float64))
 
 
@@ -169,10 +208,13 @@ def test_c4_full_bias_b2_h16_l8192_d64():
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
     scale = 1.0 / math.sqrt(D)
-    for b, h in ((0, 0), (1, 9), (0, 15)):
-        rows = [0, 255, 256, 5000, L - 1]
+    for b, h in ((0, 0), (0, 15)):
+        rows = _tiles(L)
         brow = _np(bias[b, h, rows])
         _check_rows(q, k, v, None, out, None, b, h, rows, scale=scale, bias_row=brow)
+    bslice = _np(bias[1, 9])
+    _check_slice(q, k, v, None, out, None, 1, 9, scale=scale,
+                 bias_rows=lambda r0, r1: bslice[r0:r1])
 
 
 def test_c5_block_sparse_row_bias_b1_h8_l32768_d64():
@@ -194,11 +236,73 @@ def test_c5_block_sparse_row_bias_b1_h8_l32768_d64():
     dout = _randn(gen, B, H, L, D)
     out = _fwd_bwd(q, k, v, dout, bias=bias, mask=mask)
     scale = 1.0 / math.sqrt(D)
-    for h in (0, 5):
-        rows = [0, 127, 128, 20000, L - 1]
-        mrows = np.repeat(np.repeat(blk[np.asarray(rows) // 128], 128, axis=1), 1, axis=0)
-        brow = _np(bias[0, h, 0])
-        _check_rows(q, k, v, dout, out, q.grad, 0, h, rows, scale=scale,
-                    bias_row=brow[None, :].repeat(len(rows), 0), mask_row=mrows)
+
+    def keep_rows(r0, r1):
+        return np.repeat(blk[np.arange(r0, r1) // 128], 128, axis=1)
+
+    rows = _tiles(L)
+    brow = _np(bias[0, 0, 0])
+    _check_rows(q, k, v, dout, out, q.grad, 0, 0, rows, scale=scale,
+                bias_row=brow[None, :].repeat(len(rows), 0),
+                mask_row=np.repeat(blk[np.asarray(rows) // 128], 128, axis=1))
+    h = 5
+    _check_slice(q, k, v, dout, out, (q.grad, k.grad, v.grad), 0, h, scale=scale,
+                 keep_rows=keep_rows, bias_key=_np(bias[0, h, 0]),
+                 dbias_col=bias.grad[0, h, 0], chunk=128)
     _identities(k.grad, v.grad, dout, torch.ones(B, H, L, device=_dev(), dtype=torch.float64),
                 dbias=bias.grad[0, :, 0, :])
+
+
+# --- more than 1024 tiles per row or column --------------------------------
+# Blocks keep the list of their active tiles in LDS for up to 1024 tiles;
+# longer problems classify each tile inside the loop instead.
+
+
+def test_key_padding_more_than_1024_key_tiles():
+    """Lk = 66,000 (1,032 key tiles of 64): the forward and dQ kernels run
+    without the listed tiles.  Key padding per batch, query tails."""
+    B, H, Lq, Lk, D = 2, 2, 300, 66000, 64
+    print(f'[case] B{B} H{H} Lq{Lq} Lk{Lk} D{D} key padding, >1024 key tiles', flush=True)
+    gen = torch.Generator(device=_dev())
+    gen.manual_seed(SEED + 4)
+    valid = np.array([41000, 66000])
+    q = _randn(gen, B, H, Lq, D, grad=True)
+    k, v = (_randn(gen, B, H, Lk, D, grad=True) for _ in range(2))
+    dout = _randn(gen, B, H, Lq, D)
+    mask = (torch.arange(Lk, device=_dev())[None, :]
+            < torch.as_tensor(valid, device=_dev())[:, None])[:, None, None, :]
+    out = _fwd_bwd(q, k, v, dout, mask=mask)
+    scale = 1.0 / math.sqrt(D)
+    for b, h in ((0, 1), (1, 0)):
+        mrow = np.arange(Lk) < valid[b]
+        _check_slice(q, k, v, dout, out, (q.grad, k.grad, v.grad), b, h, scale=scale,
+                     keep_rows=lambda r0, r1: np.broadcast_to(mrow, (r1 - r0, Lk)),
+                     chunk=100)
+
+
+def test_block_sparse_more_than_1024_tiles_both_ways():
+    """L = 66,000 with a [1, 1, L, L] mask of 128 x 128 blocks (2 % kept plus
+    the diagonal): 1,032 query and key tiles, so the forward, dQ and dK/dV
+    kernels all run without the listed tiles; the length leaves tails."""
+    B, H, L, D = 1, 1, 66000, 64
+    print(f'[case] B{B} H{H} L{L} D{D} block-sparse, >1024 tiles', flush=True)
+    gen = torch.Generator(device=_dev())
+    gen.manual_seed(SEED + 5)
+    rng = np.random.default_rng(SEED + 5)
+    nb = -(-L // 128)
+    blk = rng.random((nb, nb)) < 0.02
+    blk[np.arange(nb), np.arange(nb)] = True
+    tb = torch.as_tensor(blk, device=_dev())
+    mask = tb.repeat_interleave(128, 0).repeat_interleave(128, 1)[:L, :L][None, None]
+    q, k, v = (_randn(gen, B, H, L, D, grad=True) for _ in range(3))
+    dout = _randn(gen, B, H, L, D)
+    out = _fwd_bwd(q, k, v, dout, mask=mask)
+    del mask, tb
+    scale = 1.0 / math.sqrt(D)
+
+    def keep_rows(r0, r1):
+        return np.repeat(blk[np.arange(r0, r1) // 128], 128, axis=1)[:, :L]
+
+    _check_slice(q, k, v, dout, out, (q.grad, k.grad, v.grad), 0, 0, scale=scale,
+                 keep_rows=keep_rows, chunk=128)
+

@@ -338,3 +338,75 @@ def test_qk_norm_matches_oracle():
     ).cpu().numpy()
     ref = O.sdpa_forward(q, k, v, qk_norm=True, acc_dtype=np.float64)
     assert relerr(out, ref) <= 1e-5
+
+
+def test_c1_configuration_fp32():
+    """BASELINE configs[0] at its exact configuration: fp32, B1 H4 L256 D64,
+    full additive bias [1,4,256,256] ~N(0,1), no mask, non-causal, default
+    scale; forward and every gradient (dbias included) against the float64
+    oracle on the whole problem at 1e-5."""
+    _check(torch.float32, 1, 4, 256, 256, 64, bias_shape=(1, 4, 256, 256), seed=101)
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32], ids=['bf16', 'f32'])
+@pytest.mark.parametrize('B,bias_shape', [
+    (8, (4, 64, 4096)),       # shared over the batch: 2 chunks of 16 pairs
+    (8, (8, 1, 64, 4096)),    # shared over heads
+    (5, (64, 4096)),          # shared over batch and heads: chunks of 16 + 4
+    (8, (1, 4, 1, 4096)),     # query-broadcast, shared over the batch
+], ids=['batch', 'head', 'both_uneven', 'qbc_batch'])
+def test_shared_bias_gradient_in_chunks(dtype, B, bias_shape):
+    """dbias of a bias shared across (batch, head) pairs, with more pairs
+    than one chunk of the reduction (the dK/dV kernel runs over the pairs in
+    chunks of 512 / key-blocks = 16 here, each followed by a fixed-order
+    reduction into an accumulator of the bias's extent)."""
+    _check(dtype, B, 4, 64, 4096, 64, bias_shape=bias_shape, mask_kind='keypad', seed=B)
+
+
+def _run_twice(dtype, B, H, s, t, d, **kw):
+    rng = np.random.default_rng(55)
+    q = _draw(rng, (B, H, s, d), dtype)
+    k = _draw(rng, (B, H, t, d), dtype)
+    v = _draw(rng, (B, H, t, d), dtype)
+    g = _to(_draw(rng, (B, H, s, d), dtype), dtype)
+    bias = _draw(rng, kw.pop('bias_shape'), dtype)
+    mask = torch.from_numpy(_make_mask(rng, kw.pop('mask_kind'), B, H, s, t)).to(_dev())
+    from nitrix_amd import scaled_dot_product_attention
+
+    runs = []
+    for _ in range(2):
+        tq, tk, tv = _to(q, dtype, True), _to(k, dtype, True), _to(v, dtype, True)
+        tb = _to(bias, dtype, True)
+        out = scaled_dot_product_attention(tq, tk, tv, bias=tb, mask=mask,
+                                           backend='hip', **kw)
+        out.backward(g)
+        torch.cuda.synchronize()
+        runs.append([out.detach(), tq.grad, tk.grad, tv.grad, tb.grad])
+    return runs
+
+
+@pytest.mark.parametrize('dtype', DTYPES, ids=IDS)
+def test_bitwise_deterministic_reruns(dtype):
+    """Two runs of forward + backward on the same inputs agree bit for bit
+    (no atomics; dbias of a shared bias summed in a fixed order), including
+    a bias shared over the batch whose gradient takes several chunks."""
+    print(f'[case] determinism {dtype}', flush=True)
+    a, b = _run_twice(dtype, 8, 4, 200, 4096, 64, bias_shape=(4, 200, 4096),
+                      mask_kind='random', causal=True)
+    for name, x, y in zip(('out', 'dq', 'dk', 'dv', 'dbias'), a, b):
+        assert torch.equal(x, y), f'{name} differs between identical runs'
+
+
+def test_in_place_change_before_backward_raises():
+    """The inputs are kept with save_for_backward: editing one in place
+    between forward and backward raises instead of giving wrong gradients."""
+    rng = np.random.default_rng(56)
+    dtype = torch.bfloat16
+    q, k, v = (_to(_draw(rng, (1, 2, 64, 64), dtype), dtype, True) for _ in range(3))
+    from nitrix_amd import scaled_dot_product_attention
+
+    out = scaled_dot_product_attention(q, k, v, backend='hip')
+    with torch.no_grad():
+        k.mul_(2.0)
+    with pytest.raises(RuntimeError, match='modified by an inplace operation'):
+        out.backward(torch.ones_like(out))

@@ -147,16 +147,50 @@ def test_broadcast_B_C_gradients_are_summed():
 @pytest.mark.parametrize('name,dtype,tol', [('bf16', torch.bfloat16, 2e-2),
                                             ('f16', torch.float16, 1e-2)])
 def test_half_precision_inputs(name, dtype, tol):
+    """bf16 / fp16 inputs: upcast at the boundary, fp32 kernels, outputs and
+    gradients cast back to the input dtype (and B / C gradients summed over
+    a broadcast batch), against the oracle and its VJP on the same rounded
+    inputs and cotangent."""
     arrs = _inputs((2,), 64, 96, 16, 31, True, 'mamba')
-    ts = _gpu(arrs, dtype)
+    arrs[3] = arrs[3][0]  # B shared over the batch
+    ts = _gpu(arrs, dtype, grad=True)
     print(f'[case] ssm {name}', flush=True)
     y = selective_scan_hip(*ts)
     assert y.dtype == dtype
-    rounded = [t.float().cpu().numpy().astype(np.float64) for t in ts]
-    want = S.selective_scan(*rounded)
-    e = relerr(y.float().cpu().numpy(), want)
+    rounded = [t.detach().float().cpu().numpy().astype(np.float64) for t in ts]
+    Bb = np.broadcast_to(rounded[3], rounded[4].shape)
+    want = S.selective_scan(rounded[0], rounded[1], rounded[2], Bb, rounded[4], rounded[5])
+    e = relerr(y.detach().float().cpu().numpy(), want)
     print(f'  y {e:.2e}', flush=True)
     assert e <= tol
+    dy = torch.from_numpy(
+        np.random.RandomState(32).standard_normal(arrs[0].shape).astype(np.float32)
+    ).to(_dev(), dtype)
+    y.backward(dy)
+    torch.cuda.synchronize()
+    wg = list(S.selective_scan_vjp(rounded[0], rounded[1], rounded[2], Bb, rounded[4],
+                                   rounded[5], dy.float().cpu().numpy().astype(np.float64)))
+    wg[3] = wg[3].sum(0)
+    for name_, t, w in zip(('dx', 'ddelta', 'dA', 'dB', 'dC', 'dD'), ts, wg):
+        assert t.grad is not None and t.grad.dtype == dtype, name_
+        assert t.grad.shape == t.shape, name_
+        e = relerr(t.grad.float().cpu().numpy(), w)
+        print(f'  {name_} {e:.2e}', flush=True)
+        assert e <= tol, f'{name_} relerr {e:.3e}'
+
+
+def test_in_place_change_before_backward_raises():
+    """The inputs are kept with save_for_backward: editing one in place
+    between forward and backward raises instead of giving wrong gradients."""
+    arrs = _inputs((2,), 40, 64, 8, 33, True)
+    ts = _gpu(arrs, torch.float32, grad=True)
+    y = selective_scan_hip(*ts)
+    with torch.no_grad():
+        ts[1].mul_(2.0)
+    # torch words it as a version-counter error or, for a view made inside
+    # the forward, as an in-place change of that view's base.
+    with pytest.raises(RuntimeError, match='inplace'):
+        y.backward(torch.ones_like(y))
 
 
 def test_deterministic():

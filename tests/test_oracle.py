@@ -408,3 +408,60 @@ def test_planted_backward_mistake_fails_fd():
     ) / (2 * eps)
     assert abs(dk[idx] - fd) < 1e-6
     assert abs(dk[idx] / 0.5 - fd) > 1e-3
+
+
+# --- the chunked single-slice oracle (full-size GPU tests) ------------------
+
+
+@pytest.mark.parametrize('case', ['bias_rows_mask', 'key_bias_causal', 'blocks', 'cross_dv'])
+def test_slice_chunked_matches_whole_slice(case):
+    """``sdpa_slice_chunked`` (row blocks, kept columns only) equals the
+    whole-matrix oracle -- pinned above by the goldens, the naive loop, the
+    invariants and finite differences -- on every output, with chunk sizes
+    that do not divide the length."""
+    rng = np.random.default_rng(31)
+    s, t, d, dv = 150, 130, 16, 16
+    causal = False
+    bias = keep = bias_key = None
+    if case == 'cross_dv':
+        dv = 24
+    q = rng.standard_normal((s, d))
+    k = rng.standard_normal((t, d))
+    v = rng.standard_normal((t, dv))
+    g = rng.standard_normal((s, dv))
+    if case == 'bias_rows_mask':
+        bias = rng.standard_normal((s, t))
+        keep = rng.random((s, t)) < 0.4
+        keep[:, 3] = True
+    elif case == 'key_bias_causal':
+        bias_key = rng.standard_normal(t)
+        causal = True
+    elif case == 'blocks':
+        blk = rng.random((-(-s // 32), -(-t // 32))) < 0.3
+        blk[np.arange(min(blk.shape)), np.arange(min(blk.shape))] = True
+        keep = np.kron(blk, np.ones((32, 32), bool))[:s, :t]
+        bias_key = rng.standard_normal(t)
+    scale = 0.3
+    full_bias = bias if bias is not None else (
+        None if bias_key is None else np.broadcast_to(bias_key, (s, t)))
+    out, lse = O.sdpa_forward_lse(q, k, v, bias=full_bias, mask=keep, scale=scale,
+                                  causal=causal, acc_dtype=np.float64)
+    dq, dk, dvv, db = O.sdpa_backward(q, k, v, g, bias=full_bias, mask=keep, scale=scale,
+                                      causal=causal, acc_dtype=np.float64)
+    for chunk in (7, 64, 1000):
+        r = O.sdpa_slice_chunked(
+            q, k, v, g, scale=scale,
+            bias_rows=None if bias is None else (lambda a, b: bias[a:b]),
+            bias_key=bias_key,
+            keep_rows=None if keep is None else (lambda a, b: keep[a:b]),
+            causal=causal, chunk=chunk)
+        for name, want in (('out', out), ('lse', lse), ('dq', dq), ('dk', dk),
+                           ('dv', dvv)):
+            np.testing.assert_allclose(r[name], want, rtol=0, atol=1e-12, err_msg=name)
+        if full_bias is not None:
+            np.testing.assert_allclose(r['dbias_col'], db.sum(axis=0), rtol=0, atol=1e-12)
+    fwd = O.sdpa_slice_chunked(q, k, v, scale=scale, bias_key=bias_key, causal=causal,
+                               bias_rows=None if bias is None else (lambda a, b: bias[a:b]),
+                               keep_rows=None if keep is None else (lambda a, b: keep[a:b]))
+    assert set(fwd) == {'out', 'lse'}
+    np.testing.assert_allclose(fwd['out'], out, rtol=0, atol=1e-12)
