@@ -116,6 +116,22 @@ int nxa_fwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
             const void* bias, const uint8_t* mask, void* o, float* lse,
             void* workspace, size_t workspace_bytes, void* stream);
 
+/* Forward that allocates nothing and takes no workspace.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory at all
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The same kernels and results as nxa_fwd; the mask's tile map
+ * goes to a static device array of NXA_NOALLOC_SCRATCH_BYTES that every GPU
+ * the library runs on holds until the process ends.  A tile map larger than
+ * that (nxa_workspace_bytes(desc, .., NXA_WS_FWD)) is NXA_E_WORKSPACE,
+ * before any launch.  The scratch keeps the last call's contents and is
+ * shared by every call on one GPU: calls that overlap on one GPU (other
+ * streams, other threads) race, so the caller serialises them.  Runs on the
+ * current device. */
+#define NXA_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int nxa_fwd_noalloc(const nxa_desc* desc, const void* q, const void* k,
+                    const void* v, const void* bias, const uint8_t* mask, void* o,
+                    float* lse, void* stream);
+
 /* Backward: dq, dk, dv (and dbias if non-NULL) of sum(dO * o).
  * dbias has the extent of bias (size 1 on the axes whose bias stride is 0)
  * with strides dbias_str (B, H, Lq; unit stride over Lk); broadcast axes are

@@ -23,6 +23,9 @@ NXA_WS_FWD = 0
 NXA_WS_BWD = 1
 NXA_WS_DBIAS = 2
 
+# static scratch of nxa_fwd_noalloc (NXA_NOALLOC_SCRATCH_BYTES)
+NXA_NOALLOC_SCRATCH_BYTES = 8 << 20
+
 NXA_OK = 0
 NXA_E_ARG = -1
 NXA_E_SHAPE = -2
@@ -48,6 +51,7 @@ EXPORTS = (
     'nxa_check',
     'nxa_workspace_bytes',
     'nxa_fwd',
+    'nxa_fwd_noalloc',
     'nxa_bwd',
     'nxa_rms_norm_fwd',
     'nxa_rms_norm_bwd',
@@ -115,6 +119,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.nxa_workspace_bytes.argtypes = [dp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
     lib.nxa_fwd.restype = ctypes.c_int
     lib.nxa_fwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
+    lib.nxa_fwd_noalloc.restype = ctypes.c_int
+    lib.nxa_fwd_noalloc.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.nxa_bwd.restype = ctypes.c_int
     lib.nxa_bwd.argtypes = [
         dp,

@@ -456,6 +456,55 @@ int check_ptrs(const void* const* ptrs, const char* const* names, int n) {
   return NXA_OK;
 }
 
+// Validation shared by the forward entry points.
+int check_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
+              const void* bias, const uint8_t* mask, const void* o) {
+  int rc = check_desc(d, bias != nullptr, mask != nullptr);
+  if (rc) return rc;
+  const void* ptrs[4] = {q, k, v, o};
+  const char* names[4] = {"q", "k", "v", "o"};
+  return check_io_ptrs(d, ptrs, names, 4);
+}
+
+int run_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
+            const void* bias, const uint8_t* mask, void* o, float* lse,
+            void* workspace, void* stream_);
+
+// ---------------------------------------------------------------------------
+// Static scratch of nxa_fwd_noalloc: a device array that every GPU the
+// library runs on holds for the life of the process.  In host code `scratch`
+// names a host-side stand-in, not device memory: its device address is looked
+// up once per device (hipGetSymbolAddress, with that device current) and only
+// that address is handed to kernels.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = NXA_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device.
+int device_scratch(void** out) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(NXA_E_LAUNCH, "nxa_fwd_noalloc: hipGetDevice failed: %s",
+                hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(NXA_E_ARG, "nxa_fwd_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (r != hipSuccess || !p)
+      return fail(NXA_E_LAUNCH, "nxa_fwd_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                  hipGetErrorString(r));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NXA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -481,15 +530,42 @@ size_t nxa_workspace_bytes(const nxa_desc* desc, int has_bias, int has_mask,
 int nxa_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
             const void* bias, const uint8_t* mask, void* o, float* lse,
             void* workspace, size_t workspace_bytes, void* stream_) {
-  int rc = check_desc(d, bias != nullptr, mask != nullptr);
+  int rc = check_fwd(d, q, k, v, bias, mask, o);
   if (rc) return rc;
-  const void* ptrs[4] = {q, k, v, o};
-  const char* names[4] = {"q", "k", "v", "o"};
-  if ((rc = check_io_ptrs(d, ptrs, names, 4))) return rc;
   const WsLayout ws = ws_layout(d, bias != nullptr, mask != nullptr, 0);
   if (ws.total > 0 && (!workspace || workspace_bytes < ws.total))
     return fail(NXA_E_WORKSPACE, "forward needs %zu workspace bytes, got %zu",
                 ws.total, workspace ? workspace_bytes : (size_t)0);
+  return run_fwd(d, q, k, v, bias, mask, o, lse, workspace, stream_);
+}
+
+int nxa_fwd_noalloc(const nxa_desc* d, const void* q, const void* k, const void* v,
+                    const void* bias, const uint8_t* mask, void* o, float* lse,
+                    void* stream_) {
+  int rc = check_fwd(d, q, k, v, bias, mask, o);
+  if (rc) return rc;
+  const WsLayout ws = ws_layout(d, bias != nullptr, mask != nullptr, 0);
+  if (ws.total > kScratchBytes)
+    return fail(NXA_E_WORKSPACE,
+                "nxa_fwd_noalloc: the mask's tile map needs %zu bytes, the static "
+                "scratch holds %zu; use nxa_fwd with a workspace",
+                ws.total, kScratchBytes);
+  void* scratch_ptr = nullptr;
+  if (ws.total > 0 && (rc = device_scratch(&scratch_ptr))) return rc;
+  return run_fwd(d, q, k, v, bias, mask, o, lse, scratch_ptr, stream_);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The forward after validation: tile map into `workspace` (when there is a
+// mask), then the forward kernel.
+int run_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
+            const void* bias, const uint8_t* mask, void* o, float* lse,
+            void* workspace, void* stream_) {
+  int rc;
+  const WsLayout ws = ws_layout(d, bias != nullptr, mask != nullptr, 0);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   nxa::Params p = base_params(d, q, k, v, bias, mask);
   p.o = o;
@@ -502,6 +578,10 @@ int nxa_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
   const int dp = padded_dim(d);
   return launch("fwd", stream, [&] { nxa::launch_fwd(p, d->io_dtype, dp, stream); });
 }
+
+}  // namespace
+
+extern "C" {
 
 int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
             const void* bias, const uint8_t* mask, const void* o,

@@ -234,3 +234,22 @@ def test_backward_rejects_broadcast_keys(lib):
 def test_profile_read_without_records(lib):
     _lib.profile_reset()
     assert _lib.profile_read('fwd') == (0.0, 0)
+
+
+def test_noalloc_forward_rejects_a_tile_map_beyond_the_scratch(lib):
+    """nxa_fwd_noalloc keeps the tile map in a static 8 MiB device array: a
+    mask whose tile map is larger is NXA_E_WORKSPACE before anything runs
+    (no GPU needed to see it)."""
+    L = 65536 + 64  # 1025 x 1025 tiles per head
+    d = _desc(B=8, H=1, Lq=L, Lk=L, D=64)
+    d.mask_str[:] = (L * L, 0, L)  # [B, 1, L, L] mask
+    need = lib.nxa_workspace_bytes(ctypes.byref(d), 0, 1, _lib.NXA_WS_FWD)
+    assert need > _lib.NXA_NOALLOC_SCRATCH_BYTES
+    ok = ctypes.c_void_p(0x2000)
+    rc = lib.nxa_fwd_noalloc(ctypes.byref(d), ok, ok, ok, None, ok, ok, None, None)
+    assert rc == _lib.NXA_E_WORKSPACE
+    assert 'static scratch' in lib.nxa_last_error().decode()
+    # and it validates like nxa_fwd
+    rc = lib.nxa_fwd_noalloc(ctypes.byref(d), None, ok, ok, None, ok, ok, None, None)
+    assert rc == _lib.NXA_E_ARG
+
