@@ -57,6 +57,19 @@ if _ROOT not in sys.path:
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_F32_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0
+
+# HBM bytes per launch of each configuration's dominant kernel, measured with
+# rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled x2 / x1 by a copy-kernel
+# calibration); the passes, the calibration and every kernel's figures are in
+# profiles/attention_hbm_traffic_c1_c5.md.  Reported as roofline.traffic.
+MEASURED_TRAFFIC = {
+    'c1': ('fwd', 2925500),
+    'c2': ('dkdv', 903454611),
+    'c3': ('dkdv', 1619534130),
+    'c4': ('fwd', 4433131261),
+    'c5': ('dkdv', 817113574),
+}
+TRAFFIC_SOURCE = 'profiles/attention_hbm_traffic_c1_c5.md (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1)'
 SEED = 2024
 
 METRIC = 'attention fwd+bwd TFLOP/s and % of bf16 MFMA peak at B8 H16 L4096 D128'
@@ -468,6 +481,15 @@ def _bench_ssm(args, torch) -> int:
     return 0
 
 
+def _measured_traffic(name: str, kernel: str) -> dict:
+    """``traffic`` (HBM bytes per launch) from the committed counter profile,
+    when it covers this configuration's dominant kernel."""
+    hit = MEASURED_TRAFFIC.get(name)
+    if hit is None or hit[0] != kernel:
+        return {}
+    return {'traffic': hit[1], 'traffic_source': TRAFFIC_SOURCE}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -577,9 +599,13 @@ def main() -> int:
             'traffic': None,
             'algorithmic_bytes': int(wl.fwd_bytes),
         }
+        roofline.update(_measured_traffic(name, 'fwd'))
     else:
+        # FLOPs of one step's launches of the kernel over their summed time
+        # (one launch per step except for chunked shared-bias gradients).
         dom_flops = per_pair[dom] * wl.kept
-        achieved = dom_flops / (kernels[dom]['avg_ms'] * 1e-3) / 1e12
+        dom_s = kernels[dom]['avg_ms'] * kernels[dom]['launches_per_step'] * 1e-3
+        achieved = dom_flops / dom_s / 1e12
         roofline = {
             'kernel': dom,
             'bound': 'mfma',
@@ -589,6 +615,7 @@ def main() -> int:
             'frac': round(achieved / peak, 4),
             'traffic': None,
         }
+        roofline.update(_measured_traffic(name, dom))
 
     cpu = None if args.no_cpu_baseline else _cpu_baseline(name, cfg)
 
