@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define NXA_VERSION 4
+#define NXA_VERSION 5
 
 /* Flags of nxa_workspace_bytes. */
 #define NXA_WS_FWD 0   /* the forward                                        */
@@ -145,6 +145,26 @@ int nxa_bwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
             const float* lse, const void* dout, void* dq, void* dk, void* dv,
             void* dbias, const int64_t* dbias_str, void* workspace,
             size_t workspace_bytes, int tilemap_ready, void* stream);
+
+/* Backward of attention on RMS-normalised q and k (qk-norm) with the norm's
+ * VJP fused into the dQ and dK kernels.  Replaces, on the fused path, the
+ * autodiff of qk_rms_norm that the reference composes around its kernel
+ * (nn/attention/__init__.py:196-197 with _reference.py:52-77).
+ * q_hat / k_hat are the normalised inputs the forward ran on
+ * (nxa_rms_norm_fwd's y, in the I/O dtype), q / k the inputs before the
+ * norm with the same strides, q_rstd / k_rstd the per-row rsqrt from
+ * nxa_rms_norm_fwd ([B, H, Lq] / [B, H, Lk] fp32, rows in the order of the
+ * descriptor's B, H, L).  dq / dk receive the gradients with respect to q
+ * and k (dx = r (dy - y mean(dy y)), y = x r in fp32, on the un-rounded dQ /
+ * dK rows); everything else as nxa_bwd.  bf16 / fp16 I/O with D, Dv <= 128
+ * and q, k materialised over B and H, else NXA_E_UNSUPPORTED. */
+int nxa_bwd_normed(const nxa_desc* desc, const void* q_hat, const void* k_hat,
+                   const void* v, const void* bias, const uint8_t* mask,
+                   const void* o, const float* lse, const void* dout,
+                   const void* q, const void* k, const float* q_rstd,
+                   const float* k_rstd, void* dq, void* dk, void* dv, void* dbias,
+                   const int64_t* dbias_str, void* workspace,
+                   size_t workspace_bytes, int tilemap_ready, void* stream);
 
 /* qk-norm: y = x * rsqrt(mean(x^2) + eps) over each row of D elements, in
  * fp32, written in `dtype` (the reference's qk_rms_norm, _reference.py:52-77,

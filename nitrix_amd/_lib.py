@@ -53,6 +53,7 @@ EXPORTS = (
     'nxa_fwd',
     'nxa_fwd_noalloc',
     'nxa_bwd',
+    'nxa_bwd_normed',
     'nxa_rms_norm_fwd',
     'nxa_rms_norm_bwd',
     'nxa_ssm_check',
@@ -126,6 +127,16 @@ def _declare(lib: ctypes.CDLL) -> None:
         dp,
         vp, vp, vp, vp, vp,  # q k v bias mask
         vp, vp, vp,  # o lse dout
+        vp, vp, vp, vp,  # dq dk dv dbias
+        ctypes.POINTER(ctypes.c_int64),  # dbias_str
+        vp, ctypes.c_size_t, ctypes.c_int, vp,
+    ]
+    lib.nxa_bwd_normed.restype = ctypes.c_int
+    lib.nxa_bwd_normed.argtypes = [
+        dp,
+        vp, vp, vp, vp, vp,  # q_hat k_hat v bias mask
+        vp, vp, vp,  # o lse dout
+        vp, vp, vp, vp,  # q k q_rstd k_rstd
         vp, vp, vp, vp,  # dq dk dv dbias
         ctypes.POINTER(ctypes.c_int64),  # dbias_str
         vp, ctypes.c_size_t, ctypes.c_int, vp,

@@ -80,6 +80,30 @@ def qk_rms_norm(z: torch.Tensor) -> torch.Tensor:
     return (zf * torch.rsqrt(ms + _QK_RMS_EPS)).to(z.dtype)
 
 
+def _rms_norm_rows(x: torch.Tensor):
+    """``nxa_rms_norm_fwd`` over the rows of ``x``: returns ``(y, x2, rstd)``
+    with ``y`` normalised in ``x.dtype`` (shape of ``x``, contiguous), ``x2``
+    the rows of ``x`` as a contiguous ``[rows, d]`` tensor (a view of ``x``
+    when ``x`` is already laid out so) and ``rstd`` the fp32 per-row
+    ``rsqrt(mean(x^2) + eps)``."""
+    d = x.shape[-1]
+    epc = 4 if x.dtype == torch.float32 else 8
+    x2 = x.reshape(-1, d)
+    if not x2.is_contiguous() or x2.data_ptr() % 16 or d % epc:
+        x2 = x2.contiguous()
+    rows = x2.shape[0]
+    y = torch.empty((rows, d), dtype=x.dtype, device=x.device)
+    rstd = torch.empty((rows,), dtype=torch.float32, device=x.device)
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    _lib.check(
+        _lib.lib().nxa_rms_norm_fwd(
+            rows, d, _IO_DTYPES[x.dtype], x2.data_ptr(), x2.stride(0),
+            y.data_ptr(), rstd.data_ptr(), _QK_RMS_EPS, stream,
+        )
+    )
+    return y.reshape(x.shape), x2, rstd
+
+
 class _RmsNormHip(torch.autograd.Function):
     """qk-norm in one HIP pass per direction (``nxa_rms_norm_fwd`` /
     ``nxa_rms_norm_bwd``): the same math as :func:`qk_rms_norm` (fp32, cast
@@ -87,24 +111,10 @@ class _RmsNormHip(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x):
-        d = x.shape[-1]
-        epc = 4 if x.dtype == torch.float32 else 8
-        x2 = x.reshape(-1, d)
-        if x2.stride(-1) != 1 or x2.data_ptr() % 16 or x2.stride(0) % epc:
-            x2 = x2.contiguous()
-        rows = x2.shape[0]
-        y = torch.empty((rows, d), dtype=x.dtype, device=x.device)
-        rstd = torch.empty((rows,), dtype=torch.float32, device=x.device)
-        stream = torch.cuda.current_stream(x.device).cuda_stream
-        _lib.check(
-            _lib.lib().nxa_rms_norm_fwd(
-                rows, d, _IO_DTYPES[x.dtype], x2.data_ptr(), x2.stride(0),
-                y.data_ptr(), rstd.data_ptr(), _QK_RMS_EPS, stream,
-            )
-        )
+        y, x2, rstd = _rms_norm_rows(x)
         ctx.save_for_backward(x2, rstd)
         ctx.shape = x.shape
-        return y.reshape(x.shape)
+        return y
 
     @staticmethod
     @once_differentiable
@@ -412,8 +422,11 @@ def _dbias_geometry(prep: _Prepared):
     return ob, oh, lq
 
 
-def _backward(prep: _Prepared, o, lse, fwd_ws, dout, want_dbias: bool):
-    """Run ``nxa_bwd``; returns flattened ``(dq, dk, dv, dbias_kernel)``."""
+def _backward(prep: _Prepared, o, lse, fwd_ws, dout, want_dbias: bool, norm=None):
+    """Run ``nxa_bwd`` (or, with ``norm = (q_raw, k_raw, q_rstd, k_rstd)``,
+    ``nxa_bwd_normed``: ``prep`` holds the normalised q / k and dq / dk are
+    taken with respect to the raw ones); returns flattened
+    ``(dq, dk, dv, dbias_kernel)``."""
     lib = _lib.lib()
     # dK / dV are written per (b, h): broadcast q / k / v are materialised.
     q = prep.q if all(x != 0 for x in prep.q.stride()[:2]) else prep.q.contiguous()
@@ -457,28 +470,22 @@ def _backward(prep: _Prepared, o, lse, fwd_ws, dout, want_dbias: bool):
             tm = prep.workspace_bytes(_lib.NXA_WS_FWD)
             ws[:tm].copy_(fwd_ws[:tm])
             ready = 1
-    _lib.check(
-        lib.nxa_bwd(
-            ctypes.byref(prep.desc),
-            _ptr(q),
-            _ptr(k),
-            _ptr(v),
-            _ptr(prep.bias),
-            _ptr(prep.mask),
-            _ptr(o),
-            _ptr(lse),
-            _ptr(dout),
-            _ptr(dq),
-            _ptr(dk),
-            _ptr(dv),
-            _ptr(dbias),
-            dbias_str,
-            _ptr(ws),
-            ws.numel(),
-            ready,
+    if norm is None:
+        rc = lib.nxa_bwd(
+            ctypes.byref(prep.desc), _ptr(q), _ptr(k), _ptr(v), _ptr(prep.bias),
+            _ptr(prep.mask), _ptr(o), _ptr(lse), _ptr(dout), _ptr(dq), _ptr(dk),
+            _ptr(dv), _ptr(dbias), dbias_str, _ptr(ws), ws.numel(), ready,
             prep.stream(),
         )
-    )
+    else:
+        q_raw, k_raw, q_rstd, k_rstd = norm
+        rc = lib.nxa_bwd_normed(
+            ctypes.byref(prep.desc), _ptr(q), _ptr(k), _ptr(v), _ptr(prep.bias),
+            _ptr(prep.mask), _ptr(o), _ptr(lse), _ptr(dout), _ptr(q_raw),
+            _ptr(k_raw), _ptr(q_rstd), _ptr(k_rstd), _ptr(dq), _ptr(dk), _ptr(dv),
+            _ptr(dbias), dbias_str, _ptr(ws), ws.numel(), ready, prep.stream(),
+        )
+    _lib.check(rc)
     return dq, dk, dv, dbias
 
 
@@ -507,24 +514,73 @@ class _SdpaHip(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, dout):
         q, k, v, bias, mask, o, lse, ws = ctx.saved_tensors
-        ctx.shapes = (tuple(q.shape), tuple(k.shape), tuple(v.shape))
         prep = _Prepared(q, k, v, bias, mask, *ctx.args)
         want_dbias = bool(ctx.needs_input_grad[3])
-        dq, dk, dv, dbias_k = _backward(
-            prep, o, lse, ws if ws.numel() else None, dout, want_dbias
+        grads = _backward(prep, o, lse, ws if ws.numel() else None, dout, want_dbias)
+        return _input_grads(prep, (q.shape, k.shape, v.shape), grads)
+
+
+def _input_grads(prep: _Prepared, shapes, grads):
+    """Flattened kernel gradients -> gradients of the caller's q, k, v, bias
+    (broadcast axes summed, as the reference's ``_unbroadcast``)."""
+    dq, dk, dv, dbias_k = grads
+    qs, ks, vs = (tuple(x) for x in shapes)
+    lead = prep.lead
+    dq = _unbroadcast(dq.reshape(*lead, prep.s, prep.d), qs)
+    dk = _unbroadcast(dk.reshape(*lead, prep.t, prep.d), ks)
+    dv = _unbroadcast(dv.reshape(*lead, prep.t, prep.dv), vs)
+    dbias = None
+    if dbias_k is not None:
+        ob, oh, lq = dbias_k.shape[:3]
+        bdims = list(prep.batch) if ob > 1 else [1] * len(prep.batch)
+        g = dbias_k.reshape(*bdims, oh, lq, prep.t)
+        dbias = _unbroadcast(g, prep.bias_shape).to(prep.bias_dtype)
+    return dq, dk, dv, dbias, None, None, None
+
+
+class _SdpaNormHip(torch.autograd.Function):
+    """Fused attention on RMS-normalised q and k (``qk_norm=True``): the
+    one-pass norm kernels, the attention forward on the normalised rows, and
+    a backward (``nxa_bwd_normed``) whose dQ / dK kernels apply the norm's
+    VJP to their finished rows, so no normalised gradient makes an extra
+    round trip through memory.  The forward is the one of the composed path
+    (the reference normalises in the I/O dtype before its kernel,
+    ``nn/attention/__init__.py:196-197``)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bias, mask, scale, causal):
+        qn, q2, rq = _rms_norm_rows(q)
+        kn, k2, rk = _rms_norm_rows(k)
+        prep = _Prepared(qn, kn, v, bias, mask, scale, causal)
+        o, lse, ws = _forward(prep, for_bwd=any(ctx.needs_input_grad[:4]))
+        ctx.args = (scale, causal)
+        ctx.save_for_backward(
+            q, k, v, bias, mask, qn, kn, q2, k2, rq, rk, o, lse,
+            ws if ws is not None else torch.empty(0),
         )
-        qs, ks, vs = ctx.shapes
-        lead = prep.lead
-        dq = _unbroadcast(dq.reshape(*lead, prep.s, prep.d), qs)
-        dk = _unbroadcast(dk.reshape(*lead, prep.t, prep.d), ks)
-        dv = _unbroadcast(dv.reshape(*lead, prep.t, prep.dv), vs)
-        dbias = None
-        if dbias_k is not None:
-            ob, oh, lq = dbias_k.shape[:3]
-            bdims = list(prep.batch) if ob > 1 else [1] * len(prep.batch)
-            g = dbias_k.reshape(*bdims, oh, lq, prep.t)
-            dbias = _unbroadcast(g, prep.bias_shape).to(prep.bias_dtype)
-        return dq, dk, dv, dbias, None, None, None
+        return o.reshape(*prep.lead, prep.s, prep.dv)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dout):
+        q, k, v, bias, mask, qn, kn, q2, k2, rq, rk, o, lse, ws = ctx.saved_tensors
+        prep = _Prepared(qn, kn, v, bias, mask, *ctx.args)
+        want_dbias = bool(ctx.needs_input_grad[3])
+        grads = _backward(prep, o, lse, ws if ws.numel() else None, dout, want_dbias,
+                          norm=(q2, k2, rq, rk))
+        return _input_grads(prep, (q.shape, k.shape, v.shape), grads)
+
+
+def _norm_fusable(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+    """Whether ``nxa_bwd_normed`` takes this qk-norm call: 16-bit I/O, head
+    dims up to 128 (the tuned kernels) and q, k not broadcast against each
+    other or v over the leading axes."""
+    if q.dtype not in (torch.bfloat16, torch.float16) or not q.is_cuda:
+        return False
+    if max(q.shape[-1], v.shape[-1]) > 128 or q.shape[-1] % 8:
+        return False
+    lead = tuple(torch.broadcast_shapes(q.shape[:-2], k.shape[:-2], v.shape[:-2]))
+    return tuple(q.shape[:-2]) == lead and tuple(k.shape[:-2]) == lead
 
 
 def scaled_dot_product_attention_hip(
@@ -577,9 +633,15 @@ def scaled_dot_product_attention(
     resolved_scale = default_scale(q.shape[-1]) if scale is None else scale
     resolved = resolve_backend(backend, q.device)
     if resolved == 'hip':
-        q_in = _qk_norm_fused(q) if qk_norm else q
-        k_in = _qk_norm_fused(k) if qk_norm else k
         try:
+            if qk_norm and _norm_fusable(q, k, v):
+                _check_tileable(q, k, v)
+                _lib.lib()
+                return _SdpaNormHip.apply(
+                    q, k, v, bias, mask, float(resolved_scale), bool(causal)
+                )
+            q_in = _qk_norm_fused(q) if qk_norm else q
+            k_in = _qk_norm_fused(k) if qk_norm else k
             return scaled_dot_product_attention_hip(
                 q_in,
                 k_in,

@@ -583,11 +583,24 @@ int run_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
 
 extern "C" {
 
-int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
+}  // extern "C"
+
+namespace {
+
+// Raw (pre-norm) q / k and their per-row rsqrt for the fused qk-norm VJP.
+struct NormArgs {
+  const void* q;
+  const void* k;
+  const float* q_rstd;
+  const float* k_rstd;
+};
+
+int run_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
             const void* bias, const uint8_t* mask, const void* o,
             const float* lse, const void* dout, void* dq, void* dk, void* dv,
             void* dbias, const int64_t* dbias_str, void* workspace,
-            size_t workspace_bytes, int tilemap_ready, void* stream_) {
+            size_t workspace_bytes, int tilemap_ready, void* stream_,
+            const NormArgs* na) {
   int rc = check_desc(d, bias != nullptr, mask != nullptr);
   if (rc) return rc;
   const void* ptrs[8] = {q, k, v, o, dout, dq, dk, dv};
@@ -627,6 +640,25 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
   // and -lse * log2(e) for its own rows and runs first; the other kernels
   // (fp32, and head dims above 128) have a pass of its own.
   const bool dq_first = d->io_dtype != NXA_F32 && padded_dim(d) <= 128;
+  if (na) {
+    if (!dq_first)
+      return fail(NXA_E_UNSUPPORTED,
+                  "fused qk-norm backward needs bf16 / fp16 I/O and head dims <= 128");
+    const void* nptrs[4] = {na->q, na->k, na->q_rstd, na->k_rstd};
+    const char* nnames[4] = {"q (raw)", "k (raw)", "q_rstd", "k_rstd"};
+    if ((rc = check_io_ptrs(d, nptrs, nnames, 2))) return rc;
+    for (int i = 2; i < 4; ++i)
+      if (!nptrs[i]) return fail(NXA_E_ARG, "%s is NULL", nnames[i]);
+    for (int i = 0; i < 2; ++i)
+      if (d->q_str[i] == 0 || d->k_str[i] == 0)
+        return fail(NXA_E_UNSUPPORTED,
+                    "fused qk-norm backward needs q and k materialised over axis %d", i);
+    p.qk_norm = 1;
+    p.qraw = na->q;
+    p.kraw = na->k;
+    p.qrstd = na->q_rstd;
+    p.krstd = na->k_rstd;
+  }
   if (!dq_first && (rc = launch("delta", stream,
                                [&] { nxa::launch_delta(p, d->io_dtype, stream); })))
     return rc;
@@ -692,6 +724,30 @@ int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
       (rc = launch("dq", stream, [&] { nxa::launch_dq(p, d->io_dtype, dp, stream); })))
     return rc;
   return NXA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nxa_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
+            const void* bias, const uint8_t* mask, const void* o,
+            const float* lse, const void* dout, void* dq, void* dk, void* dv,
+            void* dbias, const int64_t* dbias_str, void* workspace,
+            size_t workspace_bytes, int tilemap_ready, void* stream) {
+  return run_bwd(d, q, k, v, bias, mask, o, lse, dout, dq, dk, dv, dbias, dbias_str,
+                 workspace, workspace_bytes, tilemap_ready, stream, nullptr);
+}
+
+int nxa_bwd_normed(const nxa_desc* d, const void* q_hat, const void* k_hat,
+                   const void* v, const void* bias, const uint8_t* mask, const void* o,
+                   const float* lse, const void* dout, const void* q, const void* k,
+                   const float* q_rstd, const float* k_rstd, void* dq, void* dk, void* dv,
+                   void* dbias, const int64_t* dbias_str, void* workspace,
+                   size_t workspace_bytes, int tilemap_ready, void* stream) {
+  const NormArgs na{q, k, q_rstd, k_rstd};
+  return run_bwd(d, q_hat, k_hat, v, bias, mask, o, lse, dout, dq, dk, dv, dbias,
+                 dbias_str, workspace, workspace_bytes, tilemap_ready, stream, &na);
 }
 
 int nxa_rms_norm_fwd(int64_t rows, int32_t D, int32_t dtype, const void* x,

@@ -97,7 +97,50 @@ struct Params {
   int dbias_f32;       // 1: dbias points at fp32 partials, else bias dtype
   int fwd_bias;        // FwdBias mode of the 16-bit forward
   float bias_h, bias_l;  // 1/scale = bias_h + bias_l, both exact in the bias dtype
+  // qk-norm VJP fused into the dQ and dK epilogues (16-bit backward): q and k
+  // are the RMS-normalised inputs, qraw / kraw the inputs before the norm
+  // (same strides), qrstd / krstd their per-row rsqrt(mean(x^2) + eps)
+  // ([B, H, Lq] and [B, H, Lk]); dq / dk then receive the gradients with
+  // respect to the raw inputs.
+  int qk_norm;
+  const void* qraw;
+  const void* kraw;
+  const float* qrstd;
+  const float* krstd;
 };
+
+// Gradient of y = x * r (r = rsqrt(mean(x^2) + eps) over one row of n
+// elements) for the row a lane shares with lane ^ 32: dx = r (dy - y
+// mean(dy y)), with y = x r in fp32.  `gy` holds the lane's NDB x 16
+// values of dy (accumulator layout: element 4c + j of block db is column
+// db * 32 + 8c + 4g + j), `xrow` the row of x; the results overwrite gy.
+template <typename T, int NDB>
+__device__ __forceinline__ void rms_norm_vjp_rows(float (&gy)[NDB][16], const T* xrow,
+                                                  float r, int n, int g) {
+  float y[NDB][16];
+  float dot = 0.f;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int d0 = db * 32 + 8 * c + 4 * g;
+      typedef T t4 __attribute__((ext_vector_type(4)));
+      t4 xv;
+      if (d0 < n) xv = *reinterpret_cast<const t4*>(xrow + d0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float yv = d0 < n ? (float)xv[j] * r : 0.f;
+        y[db][4 * c + j] = yv;
+        dot = __builtin_fmaf(gy[db][4 * c + j], yv, dot);
+      }
+    }
+  dot += __shfl_xor(dot, 32, 64);
+  const float mean = dot / (float)n;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) gy[db][e] = r * (gy[db][e] - y[db][e] * mean);
+}
 
 // Parameter block of the qk-norm kernels.
 struct NormParams {

@@ -44,7 +44,7 @@ def test_header_declares_the_expected_api():
 def test_library_exports_every_declared_function(lib):
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.nxa_version() == 4
+    assert lib.nxa_version() == 5
 
 
 def _desc(B=2, H=3, Lq=100, Lk=70, D=64, dtype=_lib.NXA_BF16):

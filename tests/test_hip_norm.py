@@ -11,6 +11,8 @@ output ulp from the float64 value: bf16 <= 8e-3 (2^-7), fp16 <= 2e-3 (twice
 
 from __future__ import annotations
 
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -88,3 +90,109 @@ def test_attention_qk_norm_bf16_with_grads():
         e = relerr(got.float().cpu().numpy(), want)
         print(f'  {nm} relerr {e:.2e}', flush=True)
         assert e <= 2e-2, (nm, e)
+
+
+@pytest.mark.parametrize('name,B,H,s,t,d,dv,kw', [
+    ('bf16', 2, 2, 130, 96, 128, 128, {'causal': True}),
+    ('f16', 2, 3, 70, 150, 64, 64, {'mask': 'keypad'}),
+    ('bf16', 1, 2, 100, 136, 64, 32, {'bias': (1, 2, 1, 136)}),
+    ('bf16', 2, 2, 64, 200, 40, 40, {'bias': (2, 2, 64, 200), 'mask': 'random'}),
+    ('f16', 3, 1, 257, 129, 128, 64, {'bias': (129,)}),
+], ids=['bf16_causal_d128', 'f16_keypad_cross', 'bf16_rowbias_dv32', 'bf16_bias_mask_d40',
+        'f16_shared_bias_tails'])
+def test_fused_qk_norm_backward(name, B, H, s, t, d, dv, kw):
+    """qk_norm=True on the fused path with the norm's VJP inside the dQ and
+    dK kernels (``nxa_bwd_normed``): every gradient against the float64
+    chain rule through the oracle (normalise, round to the I/O dtype,
+    attention, attention VJP, norm VJP); no separate norm backward pass
+    runs."""
+    from nitrix_amd import _lib, scaled_dot_product_attention
+
+    dtype = DT[name]
+    rnd = ROUND[name]
+    rng = np.random.default_rng(zlib.crc32(repr((name, B, H, s, t, d, dv)).encode()))
+    q = rnd(rng.standard_normal((B, H, s, d)).astype(np.float32) * 3)
+    k = rnd(rng.standard_normal((B, H, t, d)).astype(np.float32) * 3)
+    v = rnd(rng.standard_normal((B, H, t, dv)).astype(np.float32))
+    g = rnd(rng.standard_normal((B, H, s, dv)).astype(np.float32))
+    bias = None if 'bias' not in kw else rnd(rng.standard_normal(kw['bias']).astype(np.float32))
+    mask = None
+    if kw.get('mask') == 'keypad':
+        valid = rng.integers(1, t + 1, size=B)
+        mask = (np.arange(t)[None, :] < valid[:, None])[:, None, None, :]
+    elif kw.get('mask') == 'random':
+        mask = rng.random((B, H, s, t)) < 0.5
+        mask[..., 0] = True
+    causal = kw.get('causal', False)
+    to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(_dev(), dtype).requires_grad_(True)  # noqa: E731
+    tq, tk, tv = to(q), to(k), to(v)
+    tb = None if bias is None else to(bias)
+    tm = None if mask is None else torch.from_numpy(mask).to(_dev())
+    print(f'[case] fused qk-norm {name} B{B} H{H} s{s} t{t} d{d} dv{dv} {kw}', flush=True)
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    try:
+        out = scaled_dot_product_attention(tq, tk, tv, bias=tb, mask=tm, causal=causal,
+                                           qk_norm=True, backend='hip')
+        out.backward(torch.from_numpy(g).to(_dev(), dtype))
+        torch.cuda.synchronize()
+        _, n_norm_bwd = _lib.profile_read('rms_norm_bwd')
+        _, n_norm_fwd = _lib.profile_read('rms_norm_fwd')
+    finally:
+        _lib.profile_enable(False)
+        _lib.profile_reset()
+    assert n_norm_fwd == 2 and n_norm_bwd == 0, (n_norm_fwd, n_norm_bwd)
+    qh = rnd(O.qk_rms_norm(q))
+    kh = rnd(O.qk_rms_norm(k))
+    ref = O.sdpa_forward(qh, kh, v, bias=bias, mask=mask, causal=causal, acc_dtype=np.float64)
+    dqh, dkh, dvr, dbr = O.sdpa_backward(qh, kh, v, g, bias=bias, mask=mask, causal=causal,
+                                         acc_dtype=np.float64)
+    dq = O.qk_rms_norm_vjp(q.astype(np.float64), dqh)
+    dk = O.qk_rms_norm_vjp(k.astype(np.float64), dkh)
+    tol = 2e-2 if name == 'bf16' else 2e-3
+    checks = [('out', out.detach(), ref), ('dq', tq.grad, dq), ('dk', tk.grad, dk),
+              ('dv', tv.grad, dvr)]
+    if bias is not None:
+        checks.append(('dbias', tb.grad, dbr))
+    for nm, got, want in checks:
+        assert got.shape == want.shape, (nm, got.shape, want.shape)
+        e = relerr(got.float().cpu().numpy(), want)
+        print(f'  {nm} relerr {e:.2e}', flush=True)
+        assert e <= tol, (nm, e)
+
+
+def test_qk_norm_outside_the_fused_backward_uses_the_norm_passes():
+    """Shapes the fused qk-norm backward does not take (fp32 I/O; q
+    broadcast over the batch) run the norm kernels as separate passes, with
+    the same results as the oracle chain."""
+    from nitrix_amd import _lib, scaled_dot_product_attention
+
+    rng = np.random.default_rng(77)
+    for dtype, qshape in ((torch.float32, (2, 2, 40, 32)), (torch.bfloat16, (1, 2, 40, 32))):
+        rnd = O.round_bf16 if dtype == torch.bfloat16 else (lambda x: x)
+        q = rnd(rng.standard_normal(qshape).astype(np.float32) * 2)
+        k = rnd(rng.standard_normal((2, 2, 50, 32)).astype(np.float32) * 2)
+        v = rnd(rng.standard_normal((2, 2, 50, 32)).astype(np.float32))
+        g = rnd(rng.standard_normal((2, 2, 40, 32)).astype(np.float32))
+        tq, tk, tv = (torch.from_numpy(a).to(_dev(), dtype).requires_grad_(True) for a in (q, k, v))
+        _lib.profile_reset()
+        _lib.profile_enable(True)
+        try:
+            out = scaled_dot_product_attention(tq, tk, tv, qk_norm=True, backend='hip')
+            out.backward(torch.from_numpy(g).to(_dev(), dtype))
+            torch.cuda.synchronize()
+            _, n_norm_bwd = _lib.profile_read('rms_norm_bwd')
+        finally:
+            _lib.profile_enable(False)
+            _lib.profile_reset()
+        assert n_norm_bwd == 2
+        qb = np.broadcast_to(q, (2, 2, 40, 32))
+        qh = rnd(O.qk_rms_norm(qb))
+        kh = rnd(O.qk_rms_norm(k))
+        dqh, dkh, dvr, _ = O.sdpa_backward(qh, kh, v, g, acc_dtype=np.float64)
+        dq = O.unbroadcast(O.qk_rms_norm_vjp(qb.astype(np.float64), dqh), q.shape)
+        dk = O.qk_rms_norm_vjp(k.astype(np.float64), dkh)
+        tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+        for nm, got, want in (('dq', tq.grad, dq), ('dk', tk.grad, dk), ('dv', tv.grad, dvr)):
+            e = relerr(got.float().cpu().numpy(), want)
+            assert e <= tol, (dtype, nm, e)
