@@ -69,6 +69,13 @@ MEASURED_TRAFFIC = {
     'c4': ('fwd', 4433131261),
     'c5': ('dkdv', 817113574),
 }
+# VALU instructions (wave64) of the selective scan's backward pass per step at
+# the ssm configuration, transcendental instructions weighted 4: the
+# rocprofv3 SQ_INSTS_VALU / SQ_INSTS_VALU_TRANS_F32 counts of its kernels in
+# profiles/selective_scan_valu_counters.md.
+SSM_BWD_VALU_WAVE_INSTS = 2.6495e8
+SSM_VALU_SOURCE = 'profiles/selective_scan_valu_counters.md (rocprofv3 SQ_INSTS_VALU, SQ_INSTS_VALU_TRANS_F32)'
+PEAK_VALU_TLANEOPS = 256 * 4 * 32 * 2.4e9 / 1e12  # 78.6 T lane-instructions/s
 TRAFFIC_SOURCE = 'profiles/attention_hbm_traffic_c1_c5.md (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1)'
 SEED = 2024
 
@@ -435,19 +442,26 @@ def _bench_ssm(args, torch) -> int:
             kernels[kname] = {'avg_ms': tot / n, 'launches_per_step': n / prof_steps}
     _lib.profile_reset()
     fwd_b, bwd_b = _ssm_bytes(Bn, L, Dm, N)
-    # The backward pass (five kernels) dominates; its compulsory bytes over
-    # its measured duration.
+    # The backward pass (five kernels) dominates and is bound by VALU issue
+    # (one exponential and a few fp32 operations per state step; its
+    # compulsory bytes move at ~10 % of HBM bandwidth).  Its VALU work per
+    # step is the counted instructions of its kernels (transcendentals
+    # weighted 4, quarter rate) times 64 lanes, over its measured duration,
+    # against 256 CUs x 4 SIMDs x 32 lanes x 2.4 GHz (the published
+    # 157.3 TFLOP/s fp32 vector rate with an FMA counted as two).
     bwd_s = kernels['ssm_bwd']['avg_ms'] * 1e-3
-    achieved = bwd_b / bwd_s / 1e9
+    lane_ops = SSM_BWD_VALU_WAVE_INSTS * 64
+    achieved = lane_ops / bwd_s / 1e12
     roofline = {
         'kernel': 'ssm_bwd (backward pass: local, carry, chunk, two reductions)',
-        'bound': 'hbm',
-        'achieved': round(achieved, 2),
-        'peak': PEAK_HBM_GBS,
-        'unit': 'GB/s',
-        'frac': round(achieved / PEAK_HBM_GBS, 4),
+        'bound': 'valu',
+        'achieved': round(achieved, 3),
+        'peak': PEAK_VALU_TLANEOPS,
+        'unit': 'Tlane-op/s',
+        'frac': round(achieved / PEAK_VALU_TLANEOPS, 4),
         'traffic': None,
-        'algorithmic_bytes': int(bwd_b),
+        'valu_source': SSM_VALU_SOURCE,
+        'compulsory_hbm_gbs': round(bwd_b / bwd_s / 1e9, 2),
     }
     cpu = None if args.no_cpu_baseline else _ssm_cpu_baseline(cfg)
     line = {
