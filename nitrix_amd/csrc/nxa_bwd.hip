@@ -1,6 +1,6 @@
 // Backward pass: delta = rowsum(O * dO), the dK/dV and dQ kernels for fp32
-// I/O and for every I/O dtype at padded head dims above 128 (the 16-bit ones
-// up to 128 live in nxa_bwd16.hip), the dbias reduction and the launchers.
+// I/O (the 16-bit ones live in nxa_bwd16.hip), the dbias reduction and the
+// launchers.
 // Two deterministic kernels
 // (no atomics): dK/dV (+ dbias) with a grid over key tiles, and dQ with a
 // grid over query tiles.  Both recompute P from the forward's LSE.
@@ -19,8 +19,8 @@ namespace nxa {
 // ndelta[b, h, q] = -sum_d O[q, d] * dO[q, d]  (fp32) and nlse2 = -lse * log2(e),
 // so the backward kernels stream both per-row values straight from memory
 // (negated: the 16-bit kernels start their MFMA accumulators at them).  The
-// kernels of this file need it; with 16-bit I/O up to DP = 128 the dQ kernel
-// computes both for its own rows instead.
+// fp32 kernels need it; with 16-bit I/O the dQ kernel computes both for its
+// own rows instead, and runs first.
 // 16 lanes per row.
 // ---------------------------------------------------------------------------
 template <typename T>
@@ -507,20 +507,13 @@ static void launch_dkdv_t(Params p, hipStream_t stream) {
 }
 
 void launch_dkdv(const Params& p, int io_dtype, int dp, hipStream_t stream) {
-  if (dp == 256) {
-    if (io_dtype == kBF16) {
-      launch_dkdv_t<bf16, 256, kOutDv>(p, stream);
-      launch_dkdv_t<bf16, 256, kOutDk>(p, stream);
-    } else if (io_dtype == kF16) {
-      launch_dkdv_t<f16, 256, kOutDv>(p, stream);
-      launch_dkdv_t<f16, 256, kOutDk>(p, stream);
-    } else {
-      launch_dkdv_t<float, 256, kOutDv>(p, stream);
-      launch_dkdv_t<float, 256, kOutDk, kColLo>(p, stream);
-      launch_dkdv_t<float, 256, kOutDk, kColHi>(p, stream);
-    }
-  } else if (io_dtype == kBF16 || io_dtype == kF16) {
+  if (io_dtype == kBF16 || io_dtype == kF16) {
     launch_dkdv16(p, io_dtype, dp, stream);
+  } else if (dp == 256) {
+    // fp32 at DP = 256: dV, then dK in two column halves.
+    launch_dkdv_t<float, 256, kOutDv>(p, stream);
+    launch_dkdv_t<float, 256, kOutDk, kColLo>(p, stream);
+    launch_dkdv_t<float, 256, kOutDk, kColHi>(p, stream);
   } else {
     if (dp == 64) launch_dkdv_t<float, 64, kOutBoth>(p, stream);
     else launch_dkdv_t<float, 128, kOutBoth>(p, stream);
@@ -534,23 +527,13 @@ static void launch_dq_t(Params p, hipStream_t stream) {
   hipLaunchKernelGGL((dq_kernel<T, DP, CW>), dim3(n), dim3(256), 0, stream, p);
 }
 
-template <typename T>
-static void launch_dq_wide(const Params& p, hipStream_t stream) {
-  if constexpr (sizeof(T) == 2) {
-    launch_dq_t<T, 256>(p, stream);
-  } else {
-    launch_dq_t<T, 256, kColLo>(p, stream);
-    launch_dq_t<T, 256, kColHi>(p, stream);
-  }
-}
-
 void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream) {
-  if (dp == 256) {
-    if (io_dtype == kBF16) launch_dq_wide<bf16>(p, stream);
-    else if (io_dtype == kF16) launch_dq_wide<f16>(p, stream);
-    else launch_dq_wide<float>(p, stream);
-  } else if (io_dtype == kBF16 || io_dtype == kF16) {
+  if (io_dtype == kBF16 || io_dtype == kF16) {
     launch_dq16(p, io_dtype, dp, stream);
+  } else if (dp == 256) {
+    // fp32 dQ at DP = 256: one pass per half of its columns.
+    launch_dq_t<float, 256, kColLo>(p, stream);
+    launch_dq_t<float, 256, kColHi>(p, stream);
   } else {
     if (dp == 64) launch_dq_t<float, 64>(p, stream);
     else launch_dq_t<float, 128>(p, stream);

@@ -538,19 +538,414 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ.  Block = 4 waves x 32 queries (128); two blocks share a CU.  Each wave
+// dK / dV at head dim 256.  Block = 4 waves x 32 keys (128), one block per
+// CU, one wave per SIMD.  A wave holds its keys' K and V stationary (128
+// registers) and accumulates dK^T and dV^T (256 registers), so it runs every
+// product of its keys itself: S = Q K^T and dP - delta = dO V^T - delta (row
+// products on the Q / dO tile, the key on the lane's column),
+// P = exp2(S c - lse2) and dS = P (dP - delta) in fp32, then
+// dV^T += dO^T P and dK^T += Q^T dS (transposed products, ds_read_b64_tr_b16
+// reads of the same tiles).  The products are ordered so that the matrix
+// core runs dP while the VALU forms P, and dV while it forms dS.  Query
+// tiles of 32 rows (Q, dO, -lse2, -delta) stream through a 3-stage LDS ring
+// by direct copies two tiles ahead, every wave copying a quarter of each
+// tile between its row products.
+// ---------------------------------------------------------------------------
+template <typename T, bool HAS_BIAS, bool CAUSAL, int DBM>
+__global__ __launch_bounds__(256, 1) void dkdv256_kernel(const Params p) {
+  using M = Mma<T>;
+  using Frag = typename M::Frag;
+  constexpr int DP = 256, EPC = 8, KC = 16;
+  constexpr int BNK = 128, BQ = 32, NW = 4, NST = 3;
+  constexpr int NC = DP / KC, NDB = DP / 32, FPB = M::FRAGS_PER_BLOCK;
+  using QS = SwzStream<DP, NW, BQ>;
+  constexpr int NCPY = 2 * QS::CNT;                 // Q and dO copies per wave per tile
+  constexpr int TILE_BYTES = BQ * DP * 2;           // 16 KB
+  constexpr int ROWS_OFF = 2 * TILE_BYTES;          // -lse2[64], then -delta[64]
+  constexpr int STAGE_BYTES = ROWS_OFF + 2 * 64 * 4;
+  __shared__ __attribute__((aligned(16))) char smem[NST * STAGE_BYTES];
+  __shared__ uint8_t tcls[kMaxBwdTiles];
+  __shared__ int sched_s[4];
+
+  const int vid = xcd_remap(blockIdx.x, p.nbh, p.nkt);
+  const int bh = p.bh0 + vid / p.nkt;
+  const int kt = vid % p.nkt;
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
+  const int g = lane >> 5, c32 = lane & 31;
+  const int kblk0 = kt * BNK;
+  const int kw0 = kblk0 + wave * 32;
+  const int key = kw0 + c32;
+  const bool kok = key < p.Lk;
+  const int kc = kok ? key : p.Lk - 1;
+
+  const T* qp = (const T*)p.q + b * p.q_str[0] + h * p.q_str[1];
+  const T* dop = (const T*)p.dout + b * p.o_str[0] + h * p.o_str[1];
+  const float* nlp = p.nlse2 + ((int64_t)b * p.H + h) * p.Lq;
+  const float* ndp = p.ndelta + ((int64_t)b * p.H + h) * p.Lq;
+  const int64_t qs = p.q_str[2], os = p.o_str[2];
+
+  // Query-tile classes (0 = nothing kept for this key block), as in dkdv16.
+  const int nq = (p.Lq + BQ - 1) / BQ;
+  const bool cls_lds = nq <= kMaxBwdTiles;
+  auto tclass_g = [&](int t) -> int {
+    const int q0 = t * BQ;
+    if (CAUSAL && q0 + BQ - 1 < kblk0) return 0;
+    if (!p.has_tilemap) return 3;
+    return tile_class(p, b, h, q0, q0 + BQ, kblk0, kblk0 + BNK);
+  };
+  if (cls_lds)
+    for (int t = tid; t < nq; t += NW * 64) tcls[t] = (uint8_t)tclass_g(t);
+  __syncthreads();
+  auto tclass = [&](int t) -> int {
+    return cls_lds ? __builtin_amdgcn_readfirstlane((int)tcls[t]) : tclass_g(t);
+  };
+  if (wave == 0) {
+    int first = nq, last = -1, cnt = 0;
+    bool all_full = true, all_part = true;
+    for (int t0 = 0; t0 < nq; t0 += 64) {
+      const int t = t0 + lane;
+      const int c = t < nq ? tclass_g(t) : 0;
+      const uint64_t m = __ballot(c & 1);
+      if (m) {
+        first = min(first, t0 + (int)__builtin_ctzll(m));
+        last = t0 + 63 - (int)__builtin_clzll(m);
+        cnt += __popcll(m);
+      }
+      all_full = all_full && __ballot((c & 1) && !(c & 2)) == 0;
+      all_part = all_part && __ballot((c & 3) == 3) == 0;
+    }
+    if (lane == 0) {
+      sched_s[0] = first;
+      sched_s[1] = cnt > 0 && last - first + 1 == cnt;
+      sched_s[2] = all_full ? 3 : all_part ? 1 : -1;
+      sched_s[3] = last;
+    }
+  }
+  __syncthreads();
+  const int t_first = __builtin_amdgcn_readfirstlane(sched_s[0]);
+  const bool dense = __builtin_amdgcn_readfirstlane(sched_s[1]) != 0;
+  const int ucls = __builtin_amdgcn_readfirstlane(sched_s[2]);
+  const int t_last = __builtin_amdgcn_readfirstlane(sched_s[3]);
+  auto next_active = [&](int t) {
+    if (dense) return max(t, t_first) <= t_last ? max(t, t_first) : nq;
+    while (t < nq && !(tclass(t) & 1)) ++t;
+    return t;
+  };
+
+  // Stationary B operands of this lane's key: K (for S) and V (for dP).
+  Frag kf[NC], vf[NC];
+  {
+    const T* ks = (const T*)p.k + b * p.k_str[0] + h * p.k_str[1] + (int64_t)kc * p.k_str[2];
+    const T* vs = (const T*)p.v + b * p.v_str[0] + h * p.v_str[1] + (int64_t)kc * p.v_str[2];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = c * KC + g * EPC;
+      kf[c] = (kok && d < p.D) ? ld16(ks + d) : zero_frag<T>();
+      vf[c] = (kok && d < p.Dv) ? ld16(vs + d) : zero_frag<T>();
+    }
+  }
+  f32x16 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
+  float colsum = 0.f;
+
+  const bool bias_rows = HAS_BIAS && p.bias_str[2] != 0;
+  const int64_t bbase = HAS_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] + kc : 0;
+  const float bkey = (HAS_BIAS && !bias_rows) ? load_bias1(p, bbase) * kLog2e : 0.f;
+  const uint8_t* mbase =
+      p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] + kc : nullptr;
+  const int64_t dbbase = b * p.dbias_str[0] + h * p.dbias_str[1] + key - p.dbias_off;
+  // Key-only terms of the logits (query-broadcast bias, key past Lk, key
+  // padding) fold into one additive term; per-row masks and biases take the
+  // element pass.
+  const bool mask_rows = p.has_mask && p.mask_str[2] != 0;
+  const bool kmasked = !kok || (p.has_mask && !mask_rows && mbase[0] == 0);
+  const float kadd = kmasked ? -INFINITY : bkey;
+  const bool use_kadd = HAS_BIAS || p.has_mask || kw0 + 32 > p.Lk;  // uniform
+
+  if constexpr (DBM == kDbFull) {
+    if (kok)
+      for (int t = 0; t < nq; ++t)
+        if (!(tclass(t) & 1))
+          for (int i = 0; i < BQ && t * BQ + i < p.Lq; ++i)
+            store_db(p, dbbase + (int64_t)(t * BQ + i) * p.dbias_str[2], 0.f);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+  // --- copies --------------------------------------------------------------------
+  QS qsm, dsm;
+  qsm.init(qs, p.D, wave, lane);
+  dsm.init(os, p.Dv, wave, lane);
+  const uint32_t lds0 = lds_offset(smem);
+  struct TileSrc {
+    i32x4 q, d, r;
+  };
+  auto tile_src = [&](int t) NXA_INLINE -> TileSrc {
+    const int q0 = t < nq ? t * BQ : p.Lq;
+    const int rows = min(p.Lq - q0, BQ);  // 0: empty ranges
+    TileSrc s;
+    s.q = make_rsrc(qp + (int64_t)q0 * qs,
+                    rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * qs + p.D) * 2) : 0u);
+    s.d = make_rsrc(dop + (int64_t)q0 * os,
+                    rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * os + p.Dv) * 2) : 0u);
+    s.r = make_rsrc((wave == 0 ? nlp : ndp) + q0, (uint32_t)max(rows, 0) * 4u);
+    return s;
+  };
+  // Copy j of a tile into stage st: j < NCPY the wave's share of Q, then of
+  // dO; j == NCPY the per-row values (-lse2 by wave 0, -delta by wave 1).
+  auto copy = [&](const TileSrc& s, int st, int j) NXA_INLINE {
+    const uint32_t at = lds0 + st * STAGE_BYTES;
+    if (j < QS::CNT)
+      dma16_buf(s.q, qsm.off[j], at + (j * NW + wave) * 1024);
+    else if (j < NCPY)
+      dma16_buf(s.d, dsm.off[j - QS::CNT], at + TILE_BYTES + ((j - QS::CNT) * NW + wave) * 1024);
+    else if (wave < 2)
+      dma4_buf(s.r, 4u * lane, at + ROWS_OFF + wave * 256);
+  };
+
+  // --- per-lane LDS read offsets (bytes) --------------------------------------------
+  // Row reads: row c32, chunk 2m + g.  The swizzle touches the low 4 chunk
+  // bits only, so chunk pairs m and m + 8 are 256 bytes apart.
+  uint32_t roff[NC / 2];
+#pragma unroll
+  for (int m = 0; m < NC / 2; ++m) roff[m] = 2 * swz_off<DP>(c32, 2 * m + g);
+  // Transposed reads; 32-column blocks db and db + 4 are 256 bytes apart.
+  const int tr_row = 4 * ((lane >> 4) >> 1) + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  uint32_t toff[NDB / 2][2];
+#pragma unroll
+  for (int db = 0; db < NDB / 2; ++db)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int col = db * 32 + tr_col;
+      toff[db][hh] = 2 * (swz_off<DP>(tr_row + 8 * hh, col >> 3) + (col & 7));
+    }
+
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  typedef __attribute__((address_space(3))) Frag lds_frag;
+  typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  auto tr_frag = [&](uint32_t a0, uint32_t a1) NXA_INLINE -> Frag {
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a0);
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a1);
+    const i16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(Frag, r);
+  };
+  auto vadd = [](uint32_t sb, uint32_t v) NXA_INLINE -> uint32_t {
+    uint32_t r;
+    asm("v_add_u32 %0, %1, %2" : "=v"(r) : "s"(sb), "v"(v));
+    return r;
+  };
+
+  // --- one query tile ------------------------------------------------------------------
+  // Tile t in stage st; the copies of a later tile (sources s, stage stn)
+  // ride along with the row products.
+  auto tile = [&](int t, int st, const TileSrc& s, int stn) NXA_INLINE {
+    const uint32_t at = lds0 + st * STAGE_BYTES;
+    const int q0 = t * BQ;
+    copy(s, stn, NCPY);
+    // Per-row values of rows 8c + 4g .. +3: -delta seeds dP, -lse2 the logits.
+    f32x16 xs, xp, rl;
+    {
+      const uint32_t rv = vadd(at, ROWS_OFF + 16 * g);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const f32x4 l4 = *(const lds_f32x4*)(uintptr_t)(rv + 32 * c);
+        const f32x4 d4 = *(const lds_f32x4*)(uintptr_t)(rv + 256 + 32 * c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          rl[4 * c + j] = l4[j];
+          xp[4 * c + j] = d4[j];
+        }
+      }
+    }
+    // Row products: j < NC is S (Q tile, K), j >= NC is dP (dO tile, V);
+    // chunk pair m = j % NC.  A fragments are read PD products ahead.
+    uint32_t ra[NC / 2], rd[NC / 2];
+#pragma unroll
+    for (int m = 0; m < NC / 2; ++m) {
+      ra[m] = vadd(at, roff[m]);
+      rd[m] = vadd(at + TILE_BYTES, roff[m]);
+    }
+    constexpr int NPA = 2 * NC, PD = 6;
+    auto afrag = [&](int j) NXA_INLINE -> Frag {
+      const int m = j % NC;
+      const uint32_t a = j < NC ? ra[m % (NC / 2)] : rd[m % (NC / 2)];
+      return *(const lds_frag*)(uintptr_t)(a + (m / (NC / 2)) * 256);
+    };
+    Frag abuf[PD];
+#pragma unroll
+    for (int j = 0; j < PD; ++j) abuf[j] = afrag(j);
+#pragma unroll
+    for (int j = 0; j < NPA; ++j) {
+      if (j == 0)
+        xs = M::first(abuf[0], kf[0]);
+      else if (j < NC)
+        M::run(xs, abuf[j % PD], kf[j]);
+      else
+        M::run(xp, abuf[j % PD], vf[j - NC]);
+      if (j + PD < NPA) abuf[j % PD] = afrag(j + PD);
+      static_assert(NPA == 4 * NCPY, "one tile copy per four row products");
+      if ((j & 3) == 3) copy(s, stn, j >> 2);
+    }
+
+    // P = exp2(S c - lse2 [+ key term]) in fp32, packed to T for dV.
+    const int cls = ucls >= 0 ? ucls : tclass(t);
+    const bool need_mask = mask_rows && !(cls & 2);
+    const bool tail = q0 + BQ > p.Lq;
+    const bool diag = CAUSAL && (kw0 + 31 > q0);
+    const bool general = need_mask || tail || diag || bias_rows;
+    auto p_pass = [&](auto gen_tag, auto add_tag) NXA_INLINE {
+      constexpr bool GEN = decltype(gen_tag)::value;
+      constexpr bool ADD = decltype(add_tag)::value;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float xv = __builtin_fmaf(xs[r], p.scale_log2, rl[r]);
+        if constexpr (ADD) xv += kadd;
+        if constexpr (GEN) {
+          const int q = q0 + 8 * (r >> 2) + 4 * g + (r & 3);
+          const int qcl = q < p.Lq ? q : p.Lq - 1;
+          if constexpr (HAS_BIAS)
+            if (bias_rows)
+              xv = __builtin_fmaf(load_bias1(p, bbase + (int64_t)qcl * p.bias_str[2]),
+                                  kLog2e, xv);
+          bool keep = q < p.Lq;
+          if (need_mask) keep = keep && mbase[(int64_t)qcl * p.mask_str[2]] != 0;
+          if (CAUSAL) keep = keep && key <= q;
+          xv = keep ? xv : -INFINITY;
+        }
+        xs[r] = fast_exp2(xv);
+      }
+    };
+    if (general)
+      p_pass(std::true_type{}, std::true_type{});
+    else if (use_kadd)
+      p_pass(std::false_type{}, std::true_type{});
+    else
+      p_pass(std::false_type{}, std::false_type{});
+    Frag pf[FPB];
+#pragma unroll
+    for (int f = 0; f < FPB; ++f) pf[f] = M::pack(xs, f);
+
+    // dV^T += dO^T P while the VALU forms dS = P (dP - delta).
+    const uint32_t tq = at, td = at + TILE_BYTES;
+    uint32_t ta[NDB / 2][2];
+#pragma unroll
+    for (int db = 0; db < NDB / 2; ++db) {
+      ta[db][0] = vadd(td, toff[db][0]);
+      ta[db][1] = vadd(td, toff[db][1]);
+    }
+#pragma unroll
+    for (int f = 0; f < FPB; ++f)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const uint32_t o = (16 * f) * (DP * 2) + (db / (NDB / 2)) * 256;
+        M::run(dv[db], tr_frag(ta[db % (NDB / 2)][0] + o, ta[db % (NDB / 2)][1] + o), pf[f]);
+      }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float ds = xs[r] * xp[r];
+      xp[r] = ds;
+      if constexpr (DBM == kDbFull) {
+        const int q = q0 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (kok && q < p.Lq) store_db(p, dbbase + (int64_t)q * p.dbias_str[2], ds);
+      }
+      if constexpr (DBM == kDbColsum) colsum += ds;
+    }
+#pragma unroll
+    for (int f = 0; f < FPB; ++f) pf[f] = M::pack(xp, f);
+    // dK^T += Q^T dS.
+#pragma unroll
+    for (int db = 0; db < NDB / 2; ++db) {
+      ta[db][0] = vadd(tq, toff[db][0]);
+      ta[db][1] = vadd(tq, toff[db][1]);
+    }
+#pragma unroll
+    for (int f = 0; f < FPB; ++f)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const uint32_t o = (16 * f) * (DP * 2) + (db / (NDB / 2)) * 256;
+        M::run(dk[db], tr_frag(ta[db % (NDB / 2)][0] + o, ta[db % (NDB / 2)][1] + o), pf[f]);
+      }
+  };
+
+  // --- tile loop -----------------------------------------------------------------
+  // Iteration i handles active tile cur (stage stc) and copies the active
+  // tile after next into the stage that the previous tile left; before the
+  // barrier that ends it, each wave waits for its own copies of the next
+  // tile.  Every wave issues the same copies per tile (empty ranges past the
+  // last active tile), so the waits are compile-time.
+  int cur = next_active(0);
+  int nxt = cur < nq ? next_active(cur + 1) : nq;
+  {
+    const TileSrc s0 = tile_src(cur), s1 = tile_src(nxt);
+#pragma unroll
+    for (int j = 0; j <= NCPY; ++j) copy(s0, 0, j);
+#pragma unroll
+    for (int j = 0; j <= NCPY; ++j) copy(s1, 1, j);
+    // Tile cur is resident (the copies of nxt may still fly).
+    if (wave < 2)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(NCPY + 1));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(NCPY));
+  }
+  barrier_nofence();
+  int stc = 0;
+  while (cur < nq) {
+    const int nn = nxt < nq ? next_active(nxt + 1) : nq;
+    const int stn = stc == 0 ? 2 : stc - 1;  // (stc + 2) % 3
+    tile(cur, stc, tile_src(nn), stn);
+    // Tile nxt resident: only the copies of nn may be in flight.
+    if (wave < 2)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(NCPY + 1));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(NCPY));
+    barrier_nofence();
+    cur = nxt;
+    nxt = nn;
+    stc = stc == 2 ? 0 : stc + 1;
+  }
+  // No copy may still be writing LDS when the block ends.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+  if (kok) {
+    T* dkp = (T*)p.dk + b * p.k_str[0] + h * p.k_str[1] + (int64_t)key * p.k_str[2];
+    T* dvp = (T*)p.dv + b * p.v_str[0] + h * p.v_str[1] + (int64_t)key * p.v_str[2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d0 = db * 32 + 8 * c + 4 * g;
+        if (d0 < p.D) store4(dkp + d0, dk[db], 4 * c, p.scale);
+        if (d0 < p.Dv) store4(dvp + d0, dv[db], 4 * c, 1.0f);
+      }
+  }
+  if constexpr (DBM == kDbColsum) {
+    const float tot = colsum + shfl_xor32(colsum);
+    if (kok && g == 0) store_db(p, dbbase, tot);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ.  Block = 4 waves x 32 queries (128); two blocks share a CU (one at
+// head dim 256, where the stationary Q and dO and the dQ accumulators need
+// a wave's 512 registers).  Each wave
 // holds its queries' Q and dO rows stationary and streams 64-key tiles:
 // S^T = K Q^T and dP^T = V dO^T put the query on the lane's column, so dS^T
 // feeds dQ^T += K^T dS^T from registers; K^T comes from ds_read_b64_tr_b16
 // reads of the row-major (swizzled) K tile.  K / V tiles reach an LDS ring
 // by direct copies through buffer resources bounded at Lk (keys past it
-// read as zero and are masked), one tile ahead at D = 128 and two at D = 64,
+// read as zero and are masked), one tile ahead at D >= 128 and two at D = 64,
 // each wave copying its share between its S / dP products.  A bias that
 // broadcasts over queries (BMODE kFbRow) enters S^T through one more MFMA
 // per 32-key block, as in the forward; other biases take the element pass.
 // ---------------------------------------------------------------------------
 template <typename T, int DP, int BMODE, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void dq16_kernel(const Params p) {
+__global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Params p) {
   using M = Mma<T>;
   using Frag = typename M::Frag;
   using MB = Mma<bf16>;  // the ones-column product of -delta
@@ -981,7 +1376,37 @@ static void launch_dkdv16_dp(const Params& p, int dp, hipStream_t stream) {
   }
 }
 
+template <typename T, bool HB, bool CA, int DBM>
+static void launch_dkdv256_t(Params p, hipStream_t stream) {
+  p.nkt = (p.Lk + 127) / 128;
+  const int n = p.nbh * p.nkt;
+  hipLaunchKernelGGL((dkdv256_kernel<T, HB, CA, DBM>), dim3(n), dim3(256), 0, stream, p);
+}
+
+template <typename T, bool CA>
+static void launch_dkdv256_db(const Params& p, hipStream_t stream) {
+  if (!p.has_bias)
+    launch_dkdv256_t<T, false, CA, kDbNone>(p, stream);
+  else if (p.dbias_mode == kDbiasFull)
+    launch_dkdv256_t<T, true, CA, kDbFull>(p, stream);
+  else if (p.dbias_mode == kDbiasColsum)
+    launch_dkdv256_t<T, true, CA, kDbColsum>(p, stream);
+  else
+    launch_dkdv256_t<T, true, CA, kDbNone>(p, stream);
+}
+
+template <typename T>
+static void launch_dkdv256(const Params& p, hipStream_t stream) {
+  if (p.causal) launch_dkdv256_db<T, true>(p, stream);
+  else launch_dkdv256_db<T, false>(p, stream);
+}
+
 void launch_dkdv16(const Params& p, int io_dtype, int dp, hipStream_t stream) {
+  if (dp == 256) {
+    if (io_dtype == kF16) launch_dkdv256<f16>(p, stream);
+    else launch_dkdv256<bf16>(p, stream);
+    return;
+  }
   if (io_dtype == kF16) launch_dkdv16_dp<f16>(p, dp, stream);
   else launch_dkdv16_dp<bf16>(p, dp, stream);
 }
@@ -1011,7 +1436,8 @@ static void launch_dq16_flags(const Params& p, hipStream_t stream) {
 template <typename T>
 static void launch_dq16_dp(const Params& p, int dp, hipStream_t stream) {
   if (dp == 64) launch_dq16_flags<T, 64>(p, stream);
-  else launch_dq16_flags<T, 128>(p, stream);
+  else if (dp == 128) launch_dq16_flags<T, 128>(p, stream);
+  else launch_dq16_flags<T, 256>(p, stream);
 }
 
 void launch_dq16(const Params& p, int io_dtype, int dp, hipStream_t stream) {

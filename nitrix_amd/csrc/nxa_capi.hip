@@ -636,12 +636,11 @@ int run_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
   p.ndelta = reinterpret_cast<float*>(wsb + ws.delta);
   p.nlse2 = reinterpret_cast<float*>(
       wsb + ws.delta + align256((size_t)d->B * d->H * d->Lq * sizeof(float)));
-  // 16-bit I/O up to a padded head dim of 128: the dQ kernel computes -delta
-  // and -lse * log2(e) for its own rows and runs first; the other kernels
-  // (fp32, and head dims above 128) have a pass of its own.
-  const bool dq_first = d->io_dtype != NXA_F32 && padded_dim(d) <= 128;
+  // 16-bit I/O: the dQ kernel computes -delta and -lse * log2(e) for its own
+  // rows and runs first; the fp32 kernels have a pass of its own.
+  const bool dq_first = d->io_dtype != NXA_F32;
   if (na) {
-    if (!dq_first)
+    if (!dq_first || padded_dim(d) > 128)
       return fail(NXA_E_UNSUPPORTED,
                   "fused qk-norm backward needs bf16 / fp16 I/O and head dims <= 128");
     const void* nptrs[4] = {na->q, na->k, na->q_rstd, na->k_rstd};

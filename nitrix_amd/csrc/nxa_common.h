@@ -334,6 +334,12 @@ template <>
 __device__ __forceinline__ int swz<128>(int r) {
   return 4 * (r & 3) + ((r >> 2) & 3);
 }
+// 256 columns: the same pattern as 128 (the row stride is a multiple of
+// the 64 banks either way, and the XOR touches only the low 4 chunk bits).
+template <>
+__device__ __forceinline__ int swz<256>(int r) {
+  return 4 * (r & 3) + ((r >> 2) & 3);
+}
 template <>
 __device__ __forceinline__ int swz<64>(int r) {
   return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
@@ -398,19 +404,19 @@ __device__ __forceinline__ void dma4_sv(const void* base, uint32_t voff, uint32_
                :: "v"(voff), "s"(base), "s"(m) : "m0");
 }
 
-// Streams 64-row XOR-swizzled [64 x DP] bf16 tiles (swz_off layout, no
-// padding) of one [nrows, D] matrix (row stride rs elements) into LDS with
-// 1 KB direct copies: a tile is DP/8 copies, each covering 512/DP whole
-// rows of global memory, and every one of the NW waves issues exactly
-// CNT = DP/8/NW of them (so per-wave copy counts are compile-time).  The
+// Streams XOR-swizzled [ROWS x DP] bf16 tiles (64 rows unless stated; swz_off
+// layout, no padding) of one [nrows, D] matrix (row stride rs elements) into
+// LDS with 1 KB direct copies: a tile is ROWS*DP/512 copies, each covering
+// 512/DP whole rows of global memory, and every one of the NW waves issues
+// exactly CNT of them (so per-wave copy counts are compile-time).  The
 // lane's source offset inside the tile is computed once.  Rows past nrows
 // are clamped to the last row (only in the tail tile) and head-dim chunks
 // past D read chunk 0 of the row: finite filler that callers mask or
 // multiply by zero.
-template <int DP, int NW>
+template <int DP, int NW, int ROWS = 64>
 struct SwzStream {
-  static constexpr int SPR = DP / 8;  // 16-byte slots per row
-  static constexpr int NI = SPR;      // 1 KB copies per 64-row tile
+  static constexpr int SPR = DP / 8;         // 16-byte slots per row
+  static constexpr int NI = ROWS * SPR / 64;  // 1 KB copies per tile
   static constexpr int CNT = NI / NW;
   static_assert(NI % NW == 0, "tile copies must split evenly over the waves");
   // Byte offset of the lane's 16 bytes inside a full tile (64 rows times the
@@ -446,7 +452,7 @@ struct SwzStream {
                                             int wave, int lane) const {
     static_assert(sizeof(E) == 2, "16-bit tiles");
     const E* base = src + (int64_t)r0 * rs;  // wave-uniform
-    if (r0 + 64 <= nrows) {
+    if (r0 + ROWS <= nrows) {
       dma16_sv(base, off[m], lds + (m * NW + wave) * 1024);
     } else {
       const int r = min(row_of(m, wave, lane), nrows - 1 - r0);

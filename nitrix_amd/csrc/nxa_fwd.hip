@@ -378,15 +378,12 @@ static void launch_fwd_flags(const Params& p, hipStream_t stream) {
 }
 
 void launch_fwd(const Params& p, int io_dtype, int dp, hipStream_t stream) {
-  if (dp == 256) {
-    if (io_dtype == kBF16) launch_fwd_flags<bf16, 256>(p, stream);
-    else if (io_dtype == kF16) launch_fwd_flags<f16, 256>(p, stream);
-    else launch_fwd_flags<float, 256>(p, stream);
-  } else if (io_dtype == kBF16 || io_dtype == kF16) {
+  if (io_dtype == kBF16 || io_dtype == kF16) {
     launch_fwd16(p, io_dtype, dp, stream);
   } else {
     if (dp == 64) launch_fwd_flags<float, 64>(p, stream);
-    else launch_fwd_flags<float, 128>(p, stream);
+    else if (dp == 128) launch_fwd_flags<float, 128>(p, stream);
+    else launch_fwd_flags<float, 256>(p, stream);
   }
 }
 

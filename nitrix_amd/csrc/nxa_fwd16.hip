@@ -90,11 +90,14 @@ __device__ __forceinline__ void vm_wait_le(int n) {
 // t+2, two ahead: the bias streams from HBM).  In-step schedule (4-wave
 // blocks, and D = 128 with full bias tiles): tile t is read only between
 // barriers t and t+1, so the stage of tile t-1 receives tile t + NST - 1.
+// Head dim 256 (4-wave blocks, one per CU): two 64 KB K / V stages, one tile
+// ahead; no bias-tile ring (LDS is full).
 template <int DP, int NW, int BMODE>
 struct FwdRing {
   static constexpr bool TILE_BIAS = BMODE == kFbTile;
+  static_assert(DP <= 128 || (NW == 4 && !TILE_BIAS), "head dim 256: 4 waves, no bias tiles");
   static constexpr bool LAG = NW == 8 && !(TILE_BIAS && DP == 128);
-  static constexpr int NST = TILE_BIAS ? (LAG ? 3 : 2) : 4;  // K/V stages
+  static constexpr int NST = DP > 128 ? 2 : TILE_BIAS ? (LAG ? 3 : 2) : 4;  // K/V stages
   static constexpr int AHEAD = LAG ? NST - 2 : NST - 1;      // K/V tiles ahead
   static constexpr int NSTB = TILE_BIAS ? (LAG ? 3 : 2) : 1;  // bias stages
   static constexpr int AHEADB = TILE_BIAS ? NSTB - 1 : 0;     // bias tiles ahead
@@ -102,9 +105,11 @@ struct FwdRing {
 
 // NW waves of 32 queries per block: 8 (ping-pong pairs on each SIMD, one
 // block per CU) or 4 (two blocks per CU; for masks that vary over queries, so
-// that a block's key-tile list is that of its own 128 rows).
+// that a block's key-tile list is that of its own 128 rows).  Head dim 256:
+// 4 waves and one block per CU, so that each wave has the 512 registers that
+// its stationary Q (64) and O (128) need.
 template <typename T, int DP, int NW, int BMODE, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64, 2) void fwd16_kernel(const Params p) {
+__global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const Params p) {
   using M = Mma<T>;
   using Frag = typename M::Frag;
   constexpr int EPC = 8, KC = 16;
@@ -674,20 +679,28 @@ static void launch_fwd16_c(const Params& p, hipStream_t stream) {
 // full bias tiles keep the 8-wave block, whose bias ring they need.
 template <typename T, int DP, int BMODE>
 static void launch_fwd16_nw(const Params& p, hipStream_t stream) {
-  if constexpr (DP == 64 && BMODE != kFbTile) {
-    if (p.has_tilemap && p.tm_rows > 1) {
-      launch_fwd16_c<T, DP, 4, BMODE>(p, stream);
-      return;
+  if constexpr (DP > 128) {
+    launch_fwd16_c<T, DP, 4, BMODE>(p, stream);
+  } else {
+    if constexpr (DP == 64 && BMODE != kFbTile) {
+      if (p.has_tilemap && p.tm_rows > 1) {
+        launch_fwd16_c<T, DP, 4, BMODE>(p, stream);
+        return;
+      }
     }
+    launch_fwd16_c<T, DP, 8, BMODE>(p, stream);
   }
-  launch_fwd16_c<T, DP, 8, BMODE>(p, stream);
 }
 
 template <typename T, int DP>
 static void launch_fwd16_flags(const Params& p, hipStream_t stream) {
   switch (p.has_bias ? p.fwd_bias : kFbNone) {
     case kFbRow: launch_fwd16_nw<T, DP, kFbRow>(p, stream); break;
-    case kFbTile: launch_fwd16_nw<T, DP, kFbTile>(p, stream); break;
+    case kFbTile:
+      // The host maps full bias tiles to the element pass above DP = 128.
+      if constexpr (DP <= 128) launch_fwd16_nw<T, DP, kFbTile>(p, stream);
+      else launch_fwd16_nw<T, DP, kFbValu>(p, stream);
+      break;
     case kFbValu: launch_fwd16_nw<T, DP, kFbValu>(p, stream); break;
     default: launch_fwd16_nw<T, DP, kFbNone>(p, stream); break;
   }
@@ -696,7 +709,8 @@ static void launch_fwd16_flags(const Params& p, hipStream_t stream) {
 template <typename T>
 static void launch_fwd16_dp(const Params& p, int dp, hipStream_t stream) {
   if (dp == 64) launch_fwd16_flags<T, 64>(p, stream);
-  else launch_fwd16_flags<T, 128>(p, stream);
+  else if (dp == 128) launch_fwd16_flags<T, 128>(p, stream);
+  else launch_fwd16_flags<T, 256>(p, stream);
 }
 
 void launch_fwd16(const Params& p, int io_dtype, int dp, hipStream_t stream) {
