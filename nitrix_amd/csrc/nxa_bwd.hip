@@ -64,38 +64,16 @@ __device__ __forceinline__ void load_tile(const T* src, int64_t rs, int r0,
   using Frag = typename Mma<T>::Frag;
   constexpr int EPC = Mma<T>::EPC;
   constexpr int CPR = DP / EPC;
-  if constexpr (sizeof(T) == 2 && TRANS) {
-    // Pairs of rows so that transposed writes are 32-bit.
 #pragma unroll
-    for (int i = tid; i < (ROWS / 2) * CPR; i += 256) {
-      const int rp = i / CPR, cc = i % CPR;
-      const int r = 2 * rp, d = cc * EPC;
-      Frag x0 = zero_frag<T>(), x1 = zero_frag<T>();
-      if (d < D) {
-        if (r0 + r < nrows) x0 = ld16(src + (int64_t)(r0 + r) * rs + d);
-        if (r0 + r + 1 < nrows) x1 = ld16(src + (int64_t)(r0 + r + 1) * rs + d);
-      }
-      *reinterpret_cast<Frag*>(&dst[r * SK + d]) = x0;
-      *reinterpret_cast<Frag*>(&dst[(r + 1) * SK + d]) = x1;
+  for (int i = tid; i < ROWS * CPR; i += 256) {
+    const int r = i / CPR, cc = i % CPR;
+    const int d = cc * EPC;
+    Frag x = zero_frag<T>();
+    if (r0 + r < nrows && d < D) x = ld16(src + (int64_t)(r0 + r) * rs + d);
+    *reinterpret_cast<Frag*>(&dst[r * SK + d]) = x;
+    if constexpr (TRANS) {
 #pragma unroll
-      for (int j = 0; j < EPC; ++j) {
-        T pair[2] = {x0[j], x1[j]};
-        *reinterpret_cast<uint32_t*>(&dstT[(d + j) * STT + r]) =
-            *reinterpret_cast<uint32_t*>(pair);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = tid; i < ROWS * CPR; i += 256) {
-      const int r = i / CPR, cc = i % CPR;
-      const int d = cc * EPC;
-      Frag x = zero_frag<T>();
-      if (r0 + r < nrows && d < D) x = ld16(src + (int64_t)(r0 + r) * rs + d);
-      *reinterpret_cast<Frag*>(&dst[r * SK + d]) = x;
-      if constexpr (TRANS) {
-#pragma unroll
-        for (int j = 0; j < EPC; ++j) dstT[(d + j) * STT + r] = x[j];
-      }
+      for (int j = 0; j < EPC; ++j) dstT[(d + j) * STT + r] = x[j];
     }
   }
 }
@@ -106,14 +84,14 @@ __device__ __forceinline__ void store_dbias(const Params& p, int64_t off,
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV (and dbias).  Block = 4 waves x 32 keys; loops over query tiles
+// dK / dV (and dbias), fp32 I/O.  Block = 4 waves x 32 keys; loops over query tiles
 // (64 queries; 32 at DP = 256, to fit LDS).  Each wave computes S = Q K^T and
 // dP = dO V^T with the key as the lane's column, so P and dS feed
 // dV^T = dO^T P and dK^T = Q^T dS as reduction operands straight from
 // registers.  OUT selects the outputs (kOutDv, kOutDk = dK and dbias, or
 // both) and CW the head-dim columns accumulated (kColAll, or one half:
-// kColLo / kColHi).  At DP = 256 dV and dK take passes of their own (fp32
-// dK two, one per half), so that the stationary K and V and one set of
+// kColLo / kColHi).  At DP = 256 dV and dK take passes of their own (dK
+// two, one per half), so that the stationary K and V and one set of
 // accumulators fit a wave's 512 registers; dbias comes with the first dK
 // pass.
 // ---------------------------------------------------------------------------
@@ -489,14 +467,10 @@ __global__ __launch_bounds__(256) void dbias_reduce_kernel(DbiasReduce r) {
 // Host launchers.
 // ---------------------------------------------------------------------------
 void launch_delta(const Params& p, int io_dtype, hipStream_t stream) {
+  (void)io_dtype;  // fp32 only: 16-bit backward passes compute it in dQ
   const int rows = p.B * p.H * p.Lq;
   const int n = (rows + 15) / 16;
-  if (io_dtype == kBF16)
-    hipLaunchKernelGGL(delta_kernel<bf16>, dim3(n), dim3(256), 0, stream, p);
-  else if (io_dtype == kF16)
-    hipLaunchKernelGGL(delta_kernel<f16>, dim3(n), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL(delta_kernel<float>, dim3(n), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(delta_kernel<float>, dim3(n), dim3(256), 0, stream, p);
 }
 
 template <typename T, int DP, int OUT, int CW = kColAll>

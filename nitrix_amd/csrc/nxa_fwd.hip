@@ -75,21 +75,19 @@ __global__ __launch_bounds__(256) void tilemap_kernel(const Params p, int MB,
 }
 
 // ---------------------------------------------------------------------------
-// Forward kernel for fp32 I/O, and for every I/O dtype at padded head dims
-// above 128 (16-bit I/O up to 128 has its own kernel with direct global->LDS
-// tile copies).  Block = 4 waves x 32 queries (128 rows).  Up to DP = 128 two
-// blocks share a CU, so one block's softmax (VALU, v_exp) overlaps the
-// other's MFMAs; at DP = 256 a block has the CU alone (one wave per SIMD,
-// up to 512 registers for the stationary Q and the O accumulators).  K/V
-// tiles (64 keys; 32 for fp32 at DP = 256, to fit LDS) stream through
-// double-buffered LDS: the next tile is fetched into registers while the
-// current one is consumed.
+// Forward kernel for fp32 I/O (16-bit I/O has its own kernel with direct
+// global->LDS tile copies).  Block = 4 waves x 32 queries (128 rows).  Up to
+// DP = 128 two blocks share a CU, so one block's softmax (VALU, v_exp)
+// overlaps the other's MFMAs; at DP = 256 a block has the CU alone (one wave
+// per SIMD, up to 512 registers for the stationary Q and the O
+// accumulators).  K/V tiles (64 keys; 32 at DP = 256, to fit LDS) stream
+// through double-buffered LDS: the next tile is fetched into registers while
+// the current one is consumed.
 //
 // Each wave computes S^T = K Q^T so that a lane owns one query row: the row
 // max / sum need one cross-lane exchange (lane l <-> l^32) and P feeds the
-// P.V product straight from registers as its reduction operand.  For 16-bit
-// I/O, V stays row-major in LDS and is read transposed with
-// ds_read_b64_tr_b16.
+// P.V product straight from registers as its reduction operand; V is stored
+// transposed in LDS.
 //
 // The running max is only raised when a row's new maximum exceeds it by more
 // than kRescaleSlack (in log2 units): P is then bounded by 2^kRescaleSlack and
@@ -103,15 +101,14 @@ template <typename T, int DP, bool HAS_BIAS, bool CAUSAL>
 __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void fwd_kernel(const Params p) {
   using M = Mma<T>;
   using Frag = typename M::Frag;
-  constexpr bool k16 = sizeof(T) == 2;
+  static_assert(sizeof(T) == 4, "fp32 I/O");
   constexpr int EPC = M::EPC, KC = M::KC;
-  constexpr int BM = 128, BN = (DP > 128 && !k16) ? 32 : 64;
-  constexpr int NKB = BN / 32;                    // 32-key blocks per tile
-  constexpr int SKK = DP + EPC;                   // K row stride (16 B pad)
-  constexpr int SKV = k16 ? DP + 32 : BN + 4;     // V row stride (16-bit: row-major,
-                                                  // 64 B pad; fp32: transposed)
+  constexpr int BM = 128, BN = DP > 128 ? 32 : 64;
+  constexpr int NKB = BN / 32;    // 32-key blocks per tile
+  constexpr int SKK = DP + EPC;   // K row stride (16 B pad)
+  constexpr int SKV = BN + 4;     // transposed V row stride
   constexpr int KSZ = BN * SKK;
-  constexpr int VSZ = k16 ? BN * SKV : DP * SKV;
+  constexpr int VSZ = DP * SKV;
   constexpr int NC = DP / KC;
   constexpr int NDB = DP / 32;
   constexpr int CPR = DP / EPC;  // 16-byte chunks per row
@@ -197,12 +194,8 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void fwd_kernel(const Params
       const int idx = tid + i * 256;
       const int r = idx / CPR, d = (idx % CPR) * EPC;
       *reinterpret_cast<Frag*>(&Ks[r * SKK + d]) = kst[i];
-      if constexpr (k16) {
-        *reinterpret_cast<Frag*>(&Vs[r * SKV + d]) = vst[i];
-      } else {
 #pragma unroll
-        for (int j = 0; j < EPC; ++j) Vs[(d + j) * SKV + r] = vst[i][j];
-      }
+      for (int j = 0; j < EPC; ++j) Vs[(d + j) * SKV + r] = vst[i][j];
     }
   };
 
@@ -310,12 +303,7 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void fwd_kernel(const Params
         const Frag pf = M::pack(s[kb], f);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          Frag a;
-          if constexpr (k16)
-            a = lds_tr_frag(Vs, SKV, kb * 32, db * 32, lane, f);
-          else
-            a = lds_frag_t<T>(&Vs[(db * 32 + c32) * SKV + kb * 32], g, f);
-          M::run(oacc[db], a, pf);
+          M::run(oacc[db], lds_frag_t<T>(&Vs[(db * 32 + c32) * SKV + kb * 32], g, f), pf);
         }
       }
 

@@ -306,3 +306,43 @@ def test_block_sparse_more_than_1024_tiles_both_ways():
     _check_slice(q, k, v, dout, out, (q.grad, k.grad, v.grad), 0, 0, scale=scale,
                  keep_rows=keep_rows, chunk=128)
 
+
+
+# --- head dim 256 ------------------------------------------------------------
+
+
+def test_head_dim_256_b4_h16_l4096():
+    """The head-dim-256 measurement workload (bench ``w256``): bf16 fwd+bwd,
+    no mask.  128 query tiles of 32 per key block in the dK/dV kernel."""
+    B, H, L, D = 4, 16, 4096, 256
+    print(f'[case] B{B} H{H} L{L} D{D}', flush=True)
+    gen = torch.Generator(device=_dev())
+    gen.manual_seed(SEED + 6)
+    q, k, v = (_randn(gen, B, H, L, D, grad=True) for _ in range(3))
+    dout = _randn(gen, B, H, L, D)
+    out = _fwd_bwd(q, k, v, dout)
+    scale = 1.0 / math.sqrt(D)
+    _check_rows(q, k, v, dout, out, q.grad, 1, 7, _tiles(L), scale=scale)
+    _check_slice(q, k, v, dout, out, (q.grad, k.grad, v.grad), 3, 12, scale=scale)
+    _identities(k.grad, v.grad, dout, torch.ones(B, H, L, device=_dev(), dtype=torch.float64))
+
+
+def test_head_dim_256_causal_key_padding_ragged():
+    """Head dim 256, causal with key padding and a ragged length (partial
+    query and key tiles, diagonal tiles, keys removed per batch)."""
+    B, H, L, D = 2, 2, 3000, 256
+    print(f'[case] B{B} H{H} L{L} D{D} causal + key padding', flush=True)
+    gen = torch.Generator(device=_dev())
+    gen.manual_seed(SEED + 7)
+    valid = np.array([2111, 3000])
+    q, k, v = (_randn(gen, B, H, L, D, grad=True) for _ in range(3))
+    dout = _randn(gen, B, H, L, D)
+    mask = (torch.arange(L, device=_dev())[None, :]
+            < torch.as_tensor(valid, device=_dev())[:, None])[:, None, None, :]
+    out = _fwd_bwd(q, k, v, dout, mask=mask, causal=True)
+    scale = 1.0 / math.sqrt(D)
+    for b, h in ((0, 1), (1, 0)):
+        mrow = np.arange(L) < valid[b]
+        _check_slice(q, k, v, dout, out, (q.grad, k.grad, v.grad), b, h, scale=scale,
+                     keep_rows=lambda r0, r1: np.broadcast_to(mrow, (r1 - r0, L)),
+                     causal=True)

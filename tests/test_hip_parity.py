@@ -173,9 +173,10 @@ def test_value_head_dim_differs(dtype, d, dv, kw):
     (136, 136, 70, 77, {'bias_shape': (2, 70, 77)}),
 ], ids=['256', '256_causal', '192_256_bias_mask', '256_64_rowbias', '136_tails'])
 def test_wide_head_dim(dtype, d, dv, s, t, kw):
-    """Head dims above 128 (padded to 256): one wave per SIMD, narrower
-    tiles, dV / dK (and for fp32 dK / dQ column halves) in passes of their
-    own."""
+    """Head dims above 128 (padded to 256): one wave per SIMD.  16-bit I/O:
+    the forward and dQ kernels with two 64 KB tile stages, dK / dV with 32-row
+    query tiles and every product of a key in one wave; fp32: dV, dK and dQ
+    column halves in passes of their own."""
     _check(dtype, 2, 2, s, t, d, dv=dv, seed=40 + d + dv, **kw)
 
 
