@@ -156,8 +156,8 @@ int nxa_bwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
  * nxa_rms_norm_fwd ([B, H, Lq] / [B, H, Lk] fp32, rows in the order of the
  * descriptor's B, H, L).  dq / dk receive the gradients with respect to q
  * and k (dx = r (dy - y mean(dy y)), y = x r in fp32, on the un-rounded dQ /
- * dK rows); everything else as nxa_bwd.  bf16 / fp16 I/O with D, Dv <= 128
- * and q, k materialised over B and H, else NXA_E_UNSUPPORTED. */
+ * dK rows); everything else as nxa_bwd.  bf16 / fp16 I/O with q, k
+ * materialised over B and H, else NXA_E_UNSUPPORTED. */
 int nxa_bwd_normed(const nxa_desc* desc, const void* q_hat, const void* k_hat,
                    const void* v, const void* bias, const uint8_t* mask,
                    const void* o, const float* lse, const void* dout,

@@ -572,12 +572,12 @@ class _SdpaNormHip(torch.autograd.Function):
 
 
 def _norm_fusable(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
-    """Whether ``nxa_bwd_normed`` takes this qk-norm call: 16-bit I/O, head
-    dims up to 128 (the tuned kernels) and q, k not broadcast against each
-    other or v over the leading axes."""
+    """Whether ``nxa_bwd_normed`` takes this qk-norm call: 16-bit I/O, a
+    tileable head dim, and q, k not broadcast against each other or v over
+    the leading axes."""
     if q.dtype not in (torch.bfloat16, torch.float16) or not q.is_cuda:
         return False
-    if max(q.shape[-1], v.shape[-1]) > 128 or q.shape[-1] % 8:
+    if max(q.shape[-1], v.shape[-1]) > _MAX_HEAD_DIM or q.shape[-1] % 8 or v.shape[-1] % 8:
         return False
     lead = tuple(torch.broadcast_shapes(q.shape[:-2], k.shape[:-2], v.shape[:-2]))
     return tuple(q.shape[:-2]) == lead and tuple(k.shape[:-2]) == lead

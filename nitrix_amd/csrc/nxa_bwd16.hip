@@ -912,15 +912,31 @@ __global__ __launch_bounds__(256, 1) void dkdv256_kernel(const Params p) {
   // No copy may still be writing LDS when the block ends.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
+  if (p.qk_norm) {
+    // dK of the raw (pre-norm) keys: the norm's VJP on the finished rows.
+    float gy[NDB][16];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) gy[db][e] = dk[db][e] * p.scale;
+    const int64_t xoff = b * p.k_str[0] + h * p.k_str[1] + (int64_t)kc * p.k_str[2];
+    const float r = p.krstd[((int64_t)b * p.H + h) * p.Lk + kc];
+    rms_norm_vjp_rows<T, NDB>(gy, (const T*)p.kraw + xoff, r, p.D, g);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) dk[db][e] = gy[db][e];
+  }
   if (kok) {
     T* dkp = (T*)p.dk + b * p.k_str[0] + h * p.k_str[1] + (int64_t)key * p.k_str[2];
     T* dvp = (T*)p.dv + b * p.v_str[0] + h * p.v_str[1] + (int64_t)key * p.v_str[2];
+    const float sc = p.qk_norm ? 1.0f : p.scale;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int d0 = db * 32 + 8 * c + 4 * g;
-        if (d0 < p.D) store4(dkp + d0, dk[db], 4 * c, p.scale);
+        if (d0 < p.D) store4(dkp + d0, dk[db], 4 * c, sc);
         if (d0 < p.Dv) store4(dvp + d0, dv[db], 4 * c, 1.0f);
       }
   }

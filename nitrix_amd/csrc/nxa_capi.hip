@@ -640,9 +640,8 @@ int run_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
   // rows and runs first; the fp32 kernels have a pass of its own.
   const bool dq_first = d->io_dtype != NXA_F32;
   if (na) {
-    if (!dq_first || padded_dim(d) > 128)
-      return fail(NXA_E_UNSUPPORTED,
-                  "fused qk-norm backward needs bf16 / fp16 I/O and head dims <= 128");
+    if (!dq_first)
+      return fail(NXA_E_UNSUPPORTED, "fused qk-norm backward needs bf16 / fp16 I/O");
     const void* nptrs[4] = {na->q, na->k, na->q_rstd, na->k_rstd};
     const char* nnames[4] = {"q (raw)", "k (raw)", "q_rstd", "k_rstd"};
     if ((rc = check_io_ptrs(d, nptrs, nnames, 2))) return rc;

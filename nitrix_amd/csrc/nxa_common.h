@@ -114,32 +114,39 @@ struct Params {
 // mean(dy y)), with y = x r in fp32.  `gy` holds the lane's NDB x 16
 // values of dy (accumulator layout: element 4c + j of block db is column
 // db * 32 + 8c + 4g + j), `xrow` the row of x; the results overwrite gy.
+// Two passes over x (the second re-reads the row, 2n bytes, from cache) so
+// that y needs no registers of its own.
 template <typename T, int NDB>
 __device__ __forceinline__ void rms_norm_vjp_rows(float (&gy)[NDB][16], const T* xrow,
                                                   float r, int n, int g) {
-  float y[NDB][16];
+  typedef T t4 __attribute__((ext_vector_type(4)));
+  auto y4 = [&](int d0, int j, const t4& xv) -> float {
+    return d0 < n ? (float)xv[j] * r : 0.f;
+  };
   float dot = 0.f;
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int d0 = db * 32 + 8 * c + 4 * g;
-      typedef T t4 __attribute__((ext_vector_type(4)));
       t4 xv;
       if (d0 < n) xv = *reinterpret_cast<const t4*>(xrow + d0);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float yv = d0 < n ? (float)xv[j] * r : 0.f;
-        y[db][4 * c + j] = yv;
-        dot = __builtin_fmaf(gy[db][4 * c + j], yv, dot);
-      }
+      for (int j = 0; j < 4; ++j) dot = __builtin_fmaf(gy[db][4 * c + j], y4(d0, j, xv), dot);
     }
   dot += __shfl_xor(dot, 32, 64);
   const float mean = dot / (float)n;
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) gy[db][e] = r * (gy[db][e] - y[db][e] * mean);
+    for (int c = 0; c < 4; ++c) {
+      const int d0 = db * 32 + 8 * c + 4 * g;
+      t4 xv;
+      if (d0 < n) xv = *reinterpret_cast<const t4*>(xrow + d0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        gy[db][4 * c + j] = r * (gy[db][4 * c + j] - y4(d0, j, xv) * mean);
+    }
 }
 
 // Parameter block of the qk-norm kernels.

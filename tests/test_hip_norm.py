@@ -98,8 +98,10 @@ def test_attention_qk_norm_bf16_with_grads():
     ('bf16', 1, 2, 100, 136, 64, 32, {'bias': (1, 2, 1, 136)}),
     ('bf16', 2, 2, 64, 200, 40, 40, {'bias': (2, 2, 64, 200), 'mask': 'random'}),
     ('f16', 3, 1, 257, 129, 128, 64, {'bias': (129,)}),
+    ('bf16', 2, 2, 150, 140, 256, 256, {'mask': 'keypad'}),
+    ('f16', 1, 2, 100, 130, 192, 256, {'causal': True, 'bias': (1, 2, 1, 130)}),
 ], ids=['bf16_causal_d128', 'f16_keypad_cross', 'bf16_rowbias_dv32', 'bf16_bias_mask_d40',
-        'f16_shared_bias_tails'])
+        'f16_shared_bias_tails', 'bf16_keypad_d256', 'f16_causal_rowbias_d192_dv256'])
 def test_fused_qk_norm_backward(name, B, H, s, t, d, dv, kw):
     """qk_norm=True on the fused path with the norm's VJP inside the dQ and
     dK kernels (``nxa_bwd_normed``): every gradient against the float64
