@@ -59,6 +59,9 @@ namespace nxa {
 
 constexpr int kFwdMaxTiles = 1024;       // key tiles listed in LDS per block
 constexpr float kFwdRescaleSlack = 8.0f;  // lazy max raise threshold (log2)
+// Half-row tile sum of P accepted without a row max: every P is then below
+// 2^15, inside the fp16 range of the packed P V operand.
+constexpr float kFwdSumLimit = 32768.0f;
 
 // max over the two 32-lane halves (lanes l and l ^ 32).
 __device__ __forceinline__ float half_max(float x) {
@@ -512,23 +515,30 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
 #pragma unroll
       for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
   };
-  // P block kb = exp2(S[kb] cc - m_ref), packed to the T reduction
-  // fragments of P V; its row sum (four chains) joins l.
+  // P = exp2(S cc - m_ref) of the tile, packed to the T reduction fragments
+  // of P V; returns this lane's half-row sum of P (four chains per block).
+  // S is left intact, so a tile can be redone against another reference.
   Frag pf[2][FPB];
-  auto exp_half = [&](int kb, float cc) NXA_INLINE {
+  auto exp_tile = [&](float cc) NXA_INLINE -> float {
     const float neg_m = (m_ref == -INFINITY) ? 0.f : -m_ref;
-    float rs[4];
+    float ts = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      S[kb][r] = fast_exp2(__builtin_fmaf(S[kb][r], cc, neg_m));
-      rs[r & 3] = r < 4 ? S[kb][r] : rs[r & 3] + S[kb][r];
+    for (int kb = 0; kb < 2; ++kb) {
+      f32x16 pt;
+      float rs[4];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        pt[r] = fast_exp2(__builtin_fmaf(S[kb][r], cc, neg_m));
+        rs[r & 3] = r < 4 ? pt[r] : rs[r & 3] + pt[r];
+      }
+      ts += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+#pragma unroll
+      for (int f = 0; f < FPB; ++f) pf[kb][f] = M::pack(pt, f);
     }
-    l_i += (rs[0] + rs[1]) + (rs[2] + rs[3]);
-#pragma unroll
-    for (int f = 0; f < FPB; ++f) pf[kb][f] = M::pack(S[kb], f);
+    return ts;
   };
 
-  // O^T += V^T P^T for tile i (P^T from exp_half).
+  // O^T += V^T P^T for tile i (P^T from exp_tile).
   constexpr int NPV = 2 * FPB * NDB;
   auto pv = [&](int i) NXA_INLINE {
     const uint32_t vt = lds0 + (i % NST) * STAGE_BYTES + TILE_BYTES;
@@ -585,17 +595,33 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     if (i < n) qk(i);
     __builtin_amdgcn_s_setprio(0);
   };
-  // VALU work of tile i: element-wise pass (general tiles), row max, lazy
-  // reference update (O is complete up to tile i-1 here), P = exp(...).
+  // VALU work of tile i: element-wise pass (general tiles), P = exp(...)
+  // and, when needed, the row max and a lazy reference update (O is
+  // complete up to tile i-1 here).
   auto valu_phase = [&](int i) NXA_INLINE {
     if (i < 0 || i >= n) return;
     const bool gen = tile_general(i);
     if (gen) mask_tile(i);
     const float cc = gen ? 1.0f : p.scale_log2;
     float alpha;
-    if (raise_ref(row_max(cc), alpha)) rescale_o(alpha);
-    exp_half(0, cc);
-    exp_half(1, cc);
+    // Optimistic pass against the current reference, no row max: kept
+    // when every half-row sum of the tile's P (32 keys) is at most 2^15
+    // (then no P exceeds 2^15); otherwise, or before a row has a
+    // reference, the tile takes the row max, raises the reference (a sum
+    // above 2^15 means a P above 2^10, so the max exceeds the reference by
+    // more than the slack) and is redone.  O and l always accumulate
+    // against the reference in force, so the result is exact either way.
+    float ts = 0.f;
+    bool redo = __any(m_ref == -INFINITY);
+    if (!redo) {
+      ts = exp_tile(cc);
+      redo = __any(!(ts <= kFwdSumLimit));
+    }
+    if (redo) {
+      if (raise_ref(row_max(cc), alpha)) rescale_o(alpha);
+      ts = exp_tile(cc);
+    }
+    l_i += ts;
   };
   if constexpr (R::LAG) {
     // Ping-pong: every tile takes two phases between block barriers.  In
