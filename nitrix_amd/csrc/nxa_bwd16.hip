@@ -185,7 +185,9 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
   const bool mask_rows = p.has_mask && p.mask_str[2] != 0;
   const bool kmasked = !kok || (p.has_mask && !mask_rows && mbase[0] == 0);
   const float kadd = kmasked ? -INFINITY : bkey;
-  const bool use_kadd = HAS_BIAS || p.has_mask || kw0 + 32 > p.Lk;  // uniform
+  // Without a bias, only waves with a nonzero key term for some lane add it
+  // (with key padding, just the block that straddles the valid length).
+  const bool use_kadd = HAS_BIAS || __any(kadd != 0.f);  // uniform
 
   // Full dbias: entries of skipped tiles are zero.
   if constexpr (DBM == kDbFull) {
@@ -665,7 +667,9 @@ __global__ __launch_bounds__(256, 1) void dkdv256_kernel(const Params p) {
   const bool mask_rows = p.has_mask && p.mask_str[2] != 0;
   const bool kmasked = !kok || (p.has_mask && !mask_rows && mbase[0] == 0);
   const float kadd = kmasked ? -INFINITY : bkey;
-  const bool use_kadd = HAS_BIAS || p.has_mask || kw0 + 32 > p.Lk;  // uniform
+  // Without a bias, only waves with a nonzero key term for some lane add it
+  // (with key padding, just the block that straddles the valid length).
+  const bool use_kadd = HAS_BIAS || __any(kadd != 0.f);  // uniform
 
   if constexpr (DBM == kDbFull) {
     if (kok)
