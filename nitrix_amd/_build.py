@@ -37,6 +37,18 @@ HIPCC_FLAGS = [
 ]
 
 
+# Code generation flags of single translation units, on top of HIPCC_FLAGS.
+# The head-dim-256 kernels run at one wave per SIMD with 512 registers; for
+# them these flags measured faster on the box (bf16 B4 H16 L4096 D256,
+# same-box A/B): the forward 11 % with MFMA operands and results forced into
+# VGPRs, dK/dV 7 % and dQ 6 % with the max-ILP machine scheduler.  Neither
+# helps the head dim 64 / 128 kernels (max-ILP is 2-4 % slower at D = 64).
+FILE_FLAGS = {
+    'nxa_fwd16_wide.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form'],
+    'nxa_bwd16_wide.hip': ['-mllvm', '-amdgpu-sched-strategy=max-ilp'],
+}
+
+
 def _hipcc() -> str:
     rocm = os.environ.get('ROCM_PATH', '/opt/rocm')
     cand = pathlib.Path(rocm) / 'bin' / 'hipcc'
@@ -49,7 +61,7 @@ def _hipcc() -> str:
 
 
 def _compile(src: pathlib.Path, obj: pathlib.Path) -> None:
-    cmd = [_hipcc(), *HIPCC_FLAGS, '-c', str(src), '-o', str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), '-c', str(src), '-o', str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(

@@ -1,5 +1,5 @@
 // Backward pass: delta = rowsum(O * dO), the dK/dV and dQ kernels for fp32
-// I/O (the 16-bit ones live in nxa_bwd16.hip), the dbias reduction and the
+// I/O (the 16-bit ones live in nxa_bwd16.h), the dbias reduction and the
 // launchers.
 // Two deterministic kernels
 // (no atomics): dK/dV (+ dbias) with a grid over key tiles, and dQ with a

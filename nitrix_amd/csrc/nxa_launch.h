@@ -16,6 +16,10 @@ void launch_dkdv(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dkdv16(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dq16(const Params& p, int io_dtype, int dp, hipStream_t stream);
+// Padded head dim 256 (16-bit I/O), in translation units of their own.
+void launch_fwd16_wide(const Params& p, int io_dtype, hipStream_t stream);
+void launch_dkdv16_wide(const Params& p, int io_dtype, hipStream_t stream);
+void launch_dq16_wide(const Params& p, int io_dtype, hipStream_t stream);
 void launch_rms_norm(const NormParams& p, int dtype, bool bwd, hipStream_t stream);
 int ssm_padded_states(int N);
 int ssm_lanes_per_channel(int NP);
