@@ -173,7 +173,17 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
-  float colsum = 0.f;
+  // Column sums of dS (dbias of a query-broadcast bias) on the matrix core:
+  // an all-ones A operand times the packed dS of each fragment adds the
+  // fragment's 16 queries into every row of csacc.
+  f32x16 csacc;
+  Frag ones;
+  if constexpr (DBM == kDbColsum) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) csacc[r] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = (T)1.0f;
+  }
 
   // Bias: a per-key constant when it broadcasts over queries, else per row.
   const bool bias_rows = HAS_BIAS && p.bias_str[2] != 0;
@@ -356,6 +366,8 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
           M::run(acc[db], tr_frag(ta[db][0] + ro, ta[db][1] + ro), pf[qb][f]);
+        if constexpr (DBM == kDbColsum)
+          if (!pw) M::run(csacc, ones, pf[qb][f]);
       }
   };
 
@@ -443,7 +455,6 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
             const int q = q0 + qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
             if (kok && q < p.Lq) store_db(p, dbbase + (int64_t)q * p.dbias_str[2], ds);
           }
-          if constexpr (DBM == kDbColsum) colsum += ds;
         }
         pf[qb][f] = M::pack(x[qb], f);
       }
@@ -539,7 +550,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
     }
   }
   if constexpr (DBM == kDbColsum) {
-    const float tot = colsum + shfl_xor32(colsum);
+    const float tot = csacc[0];  // every row holds the column sum
     if (!pw && kok && g == 0) store_db(p, dbbase, tot);
   }
 }
