@@ -20,7 +20,8 @@
 // computed once per block.
 //
 // Schedule: the two waves of a SIMD ping-pong.  Every tile takes two phases
-// between block barriers; in one phase wave w runs its matrix products
+// (one block barrier per tile, two with full bias tiles); in one phase wave
+// w runs its matrix products
 // (O += P(t-1) V(t-1), S(t) = K(t) Q^T) while wave w + 4 runs the softmax of
 // tile t-1 (VALU, v_exp), in the next they swap, so one wave of each SIMD
 // pair keeps the matrix core busy while the other works on the VALU.
@@ -629,10 +630,14 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     l_i += ts;
   };
   if constexpr (R::LAG) {
-    // Ping-pong: every tile takes two phases between block barriers.  In
-    // phase a of tile t the leading wave (w < 4) runs its matrix work while
-    // the lagging wave (w + 4, same SIMD) runs the softmax of tile t-1; in
-    // phase b they swap.
+    // Ping-pong: every tile takes two phases.  In phase a of tile t the
+    // leading wave (w < 4) runs its matrix work while the lagging wave
+    // (w + 4, same SIMD) runs the softmax of tile t-1; in phase b they swap.
+    // One block barrier per tile orders the LDS ring (tile t resident, the
+    // stage of tile t-2 free for the copies issued after it); a second one
+    // between the phases keeps the pairs in step only with full bias tiles,
+    // whose HBM stream it paces (without bias tiles it costs 1-2.5 %).
+    constexpr bool MID_BARRIER = BMODE == kFbTile;
     auto run = [&](auto lag_tag) {
       constexpr bool LAG = decltype(lag_tag)::value;
       prologue();
@@ -642,7 +647,7 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
         issue_ahead(i);
         if (LAG) valu_phase(i - 1);
         else mfma_phase(i);
-        barrier_nofence();
+        if constexpr (MID_BARRIER) barrier_nofence();
         if (LAG) mfma_phase(i);
         else valu_phase(i);
       }
