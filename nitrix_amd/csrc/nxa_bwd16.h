@@ -33,6 +33,8 @@
 namespace nxa {
 
 constexpr int kMaxBwdTiles = 1024;
+// Build-time tuning knob (-D on the compiler line): the wave priority
+// (s_setprio) of the dK/dV waves' critical chains.
 #ifndef DKDV_PRIO
 #define DKDV_PRIO 1
 #endif

@@ -54,6 +54,9 @@
 
 #include <type_traits>
 
+// Build-time tuning knobs (-D on the compiler line): the wave priority
+// (s_setprio) of the matrix phase, and how many MFMA operand fragments the
+// products read ahead of their use.
 #ifndef FWD_PRIO
 #define FWD_PRIO 1
 #endif
