@@ -69,11 +69,12 @@ MEASURED_TRAFFIC = {
     'c4': ('fwd', 4433131261),
     'c5': ('dkdv', 817113574),
 }
-# VALU instructions (wave64) of the selective scan's backward pass per step at
-# the ssm configuration, transcendental instructions weighted 4: the
+# VALU instructions (wave64) of the selective scan's backward pass (all five
+# kernels) per step at the ssm configuration, transcendental instructions
+# weighted 4: the
 # rocprofv3 SQ_INSTS_VALU / SQ_INSTS_VALU_TRANS_F32 counts of its kernels in
 # profiles/selective_scan_valu_counters.md.
-SSM_BWD_VALU_WAVE_INSTS = 2.6495e8
+SSM_BWD_VALU_WAVE_INSTS = 2.5654e8
 SSM_VALU_SOURCE = 'profiles/selective_scan_valu_counters.md (rocprofv3 SQ_INSTS_VALU, SQ_INSTS_VALU_TRANS_F32)'
 PEAK_VALU_TLANEOPS = 256 * 4 * 32 * 2.4e9 / 1e12  # 78.6 T lane-instructions/s
 TRAFFIC_SOURCE = 'profiles/attention_hbm_traffic_c1_c5.md (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1)'

@@ -238,6 +238,24 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_bwd_local_kernel(const SsmParam
   p.sdt[((int64_t)k.b * p.nc + k.c) * p.Dm + k.d] = sdt;
 }
 
+// x of lane ^ m, for a lane mask m that is a compile-time constant once the
+// callers' loops are unrolled, with every lane of the wave active.  Masks 1
+// and 2 are DPP quad permutes (the following add takes the operand straight
+// from the permute), 4 to 16 ds_swizzle xor patterns (within 32 lanes); both
+// need no address arithmetic, unlike ds_bpermute.  Mask 32 falls back to
+// the generic shuffle.
+__device__ __forceinline__ float lane_xor(float x, int m) {
+  const int xi = __float_as_int(x);
+  if (m == 1)
+    return __int_as_float(__builtin_amdgcn_mov_dpp(xi, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+  if (m == 2)
+    return __int_as_float(__builtin_amdgcn_mov_dpp(xi, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+  if (m == 4) return __int_as_float(__builtin_amdgcn_ds_swizzle(xi, 0x1F | (4 << 10)));
+  if (m == 8) return __int_as_float(__builtin_amdgcn_ds_swizzle(xi, 0x1F | (8 << 10)));
+  if (m == 16) return __int_as_float(__builtin_amdgcn_ds_swizzle(xi, 0x1F | (16 << 10)));
+  return __shfl_xor(x, m, 64);
+}
+
 // Sums v[0..V) over the lanes of a wave that share lane % LPC (the lanes
 // of one state group, one per channel).  log2(V) halving exchanges (masks
 // 32 down to 2^SH, SH = 6 - log2(V)) leave each lane one value index,
@@ -269,13 +287,13 @@ __device__ __forceinline__ float wave_sum_scatter(float (&v)[V], int lane) {
         const float lo = v[i], hi = v[i + half];
         const float keep = up ? hi : lo;
         const float send = up ? lo : hi;
-        v[i] = keep + __shfl_xor(send, m, 64);
+        v[i] = keep + lane_xor(send, m);
       }
     }
   }
   float s = v[0];
 #pragma unroll
-  for (int m = 32 / V; m >= LPC; m /= 2) s += __shfl_xor(s, m, 64);
+  for (int m = 32 / V; m >= LPC; m /= 2) s += lane_xor(s, m);
   return s;
 }
 
@@ -360,8 +378,8 @@ __global__ __launch_bounds__(kSsmBlock) void ssm_bwd_chunk_kernel(const SsmParam
         }
 #pragma unroll
         for (int m = 1; m < LPC; m *= 2) {
-          sgb += __shfl_xor(sgb, m, 64);
-          sga += __shfl_xor(sga, m, 64);
+          sgb += lane_xor(sgb, m);
+          sga += lane_xor(sga, m);
         }
         const float dx = __builtin_fmaf(dt, sgb, Dd * dyv);
         const float ddt = __builtin_fmaf(xv, sgb, kLn2 * sga);
