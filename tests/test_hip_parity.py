@@ -180,6 +180,91 @@ def test_wide_head_dim(dtype, d, dv, s, t, kw):
     _check(dtype, 2, 2, s, t, d, dv=dv, seed=40 + d + dv, **kw)
 
 
+def _check_levels(dtype, B, H, s, t, d, levels, *, causal=False, mask_kind=None, seed=0):
+    """Forward and gradients against the float64 oracle for q, k whose logits
+    follow `levels` (natural-log units, one value per 64-key tile) along the
+    keys: q_i = 8 u + noise, k_j = levels[j // 64] sqrt(d) / 8 u + noise with
+    u a unit vector, so that with the default scale 1/sqrt(d) the logit
+    scale q_i . k_j is levels[j // 64] plus noise of order one."""
+    rng = np.random.default_rng(seed)
+    u = np.ones(d, np.float32) / np.sqrt(d)
+    lv = np.repeat(np.asarray(levels, np.float32), 64)[:t]
+    q = 8.0 * u[None, None, None, :] + 0.5 * rng.standard_normal((B, H, s, d)).astype(np.float32)
+    k = (lv[None, None, :, None] * u[None, None, None, :] * (np.sqrt(d) / 8.0)
+         + 0.5 * rng.standard_normal((B, H, t, d)).astype(np.float32))
+    v = rng.standard_normal((B, H, t, d)).astype(np.float32)
+    g = rng.standard_normal((B, H, s, d)).astype(np.float32)
+    rnd = {torch.bfloat16: O.round_bf16, torch.float16: O.round_f16}.get(dtype, lambda x: x)
+    q, k, v, g = rnd(q), rnd(k), rnd(v), rnd(g)
+    mask = _make_mask(rng, mask_kind, B, H, s, t)
+    scale = 1.0 / np.sqrt(d)
+    tq, tk, tv = _to(q, dtype, True), _to(k, dtype, True), _to(v, dtype, True)
+    tm = None if mask is None else torch.from_numpy(mask).to(_dev())
+    from nitrix_amd import scaled_dot_product_attention
+
+    logits = scale * np.einsum('bhsd,bhtd->bhst', q.astype(np.float64), k.astype(np.float64))
+    print(f'[case] levels {dtype} B{B} H{H} s{s} t{t} d{d} causal={causal} mask={mask_kind} '
+          f'logits [{logits.min():.0f}, {logits.max():.0f}]', flush=True)
+    out = scaled_dot_product_attention(tq, tk, tv, mask=tm, causal=causal, backend='hip')
+    ref = O.sdpa_forward(q, k, v, mask=mask, causal=causal, acc_dtype=np.float64)
+    # fp32: scores this large are ill-conditioned in fp32 itself -- |q . k|
+    # reaches ~3,500 (ulp 2.4e-4) before the scale, so the logits carry
+    # ~1e-4 of rounding whatever the kernel; a reference that failed to
+    # follow the row maximum would be off by order one.
+    tol = 1e-3 if dtype == torch.float32 else REL[dtype]
+    e = relerr(out.detach().float().cpu().numpy(), ref)
+    print(f'  out relerr {e:.2e}', flush=True)
+    assert e <= tol, f'out relerr {e:.3e}'
+    out.backward(_to(g, dtype))
+    torch.cuda.synchronize()
+    dq, dk, dv, _ = O.sdpa_backward(q, k, v, g, mask=mask, causal=causal, acc_dtype=np.float64)
+    # dQ_i = scale sum_j dS_ij k_j: along u the keys' large shared component
+    # meets sum_j dS_ij = 0, so the 16-bit rounding of dS in the dQ product
+    # is amplified by |k . u| / |noise| (~90 here) there -- a property of
+    # any bf16 / fp16 backward, not of the row reference.  dQ is compared
+    # orthogonal to u; dK and dV in full.
+    def perp(x):
+        return x - (x @ u.astype(np.float64))[..., None] * u.astype(np.float64)
+    errs = {}
+    for name, got, want in (('dq_perp_u', tq.grad, dq), ('dk', tk.grad, dk), ('dv', tv.grad, dv)):
+        a = got.float().cpu().numpy().astype(np.float64)
+        if name == 'dq_perp_u':
+            a, want = perp(a), perp(want)
+        errs[name] = relerr(a, want)
+        print(f'  {name} relerr {errs[name]:.2e}', flush=True)
+    for name, e in errs.items():
+        assert e <= tol, f'{name} relerr {e:.3e}'
+
+
+# Tile levels that rise steeply (every tile's row maximum exceeds the last by
+# ~25 in natural-log units, so the forward's optimistic pass fails and the
+# reference is raised on every tile), fall (the first tile holds the maximum),
+# and jump up and down.
+LEVELS = {
+    'rising': [25.0 * i for i in range(16)],
+    'falling': [25.0 * (15 - i) for i in range(16)],
+    'jumps': [0, 60, -40, 90, 10, 150, 149, 30, 200, -100, 210, 0, 260, 255, 5, 300],
+}
+
+
+@pytest.mark.parametrize('dtype', DTYPES, ids=IDS)
+@pytest.mark.parametrize('pattern', sorted(LEVELS))
+def test_logits_far_above_the_running_max(dtype, pattern):
+    """Rows whose maximum grows (or drops) by orders of magnitude from one
+    key tile to the next: the forward's row reference must follow, with
+    every output and gradient as the oracle's."""
+    _check_levels(dtype, 1, 2, 96, 1000, 64, LEVELS[pattern], seed=90)
+
+
+@pytest.mark.parametrize('dtype', DTYPES, ids=IDS)
+@pytest.mark.parametrize('d,kw', [(128, {'mask_kind': 'keypad'}), (128, {'causal': True}),
+                                  (256, {})], ids=['d128_keypad', 'd128_causal', 'd256'])
+def test_rising_logits_other_kernels(dtype, d, kw):
+    t = 700 if kw.get('causal') else 1000
+    _check_levels(dtype, 2, 1, t if kw.get('causal') else 130, t, d, LEVELS['rising'],
+                  seed=91, **kw)
+
+
 @pytest.mark.parametrize('dtype', DTYPES, ids=IDS)
 @pytest.mark.parametrize('s,t', [(256, 256), (200, 130), (96, 300)])
 def test_causal(dtype, s, t):
