@@ -33,6 +33,91 @@
 namespace nxa {
 
 constexpr int kMaxBwdTiles = 1024;
+
+// Active query tiles of one key block (tile class & 1: something kept).
+// Wave 0 compacts them, in order, into an LDS list, so the tile loop finds
+// the k-th active tile with one LDS read (issued an iteration ahead) instead
+// of a scan over the classes; a contiguous run (no mask, key padding,
+// causal) needs no read at all.  Above kMaxBwdTiles query tiles no list is
+// kept and the loop scans the tile map itself.
+struct QTiles {
+  int nq, first, cnt, ucls;
+  bool listed, dense;
+  const uint16_t* act;   // active tiles, in order (listed)
+  const uint8_t* acls;   // their classes
+  const uint8_t* cls;    // class of every tile (listed)
+  // Active tile k, given active tile k - 1 = prev (-1 for k = 0); nq past
+  // the last.
+  template <typename F>
+  __device__ __forceinline__ int tile(int k, int prev, F&& cg) const {
+    if (dense) return k < cnt ? first + k : nq;
+    if (listed) return k < cnt ? __builtin_amdgcn_readfirstlane((int)act[k]) : nq;
+    int t = prev + 1;
+    while (t < nq && !(cg(t) & 1)) ++t;
+    return t;
+  }
+  // Class of active tile k (= t): uniform over the block's tiles when ucls >= 0.
+  template <typename F>
+  __device__ __forceinline__ int klass(int k, int t, F&& cg) const {
+    if (ucls >= 0) return ucls;
+    return listed ? __builtin_amdgcn_readfirstlane((int)acls[k]) : cg(t);
+  }
+  template <typename F>
+  __device__ __forceinline__ bool active(int t, F&& cg) const {
+    return ((listed ? (int)cls[t] : cg(t)) & 1) != 0;
+  }
+};
+
+// Builds the list (every thread of the block calls it; two block barriers).
+// cg(t) is the class of query tile t for this key block.
+template <typename F>
+__device__ QTiles build_qtiles(uint16_t* act, uint8_t* acls, uint8_t* cls, int* hdr,
+                               int nq, int tid, int nthreads, F&& cg) {
+  const bool listed = nq <= kMaxBwdTiles;
+  if (listed)
+    for (int t = tid; t < nq; t += nthreads) cls[t] = (uint8_t)cg(t);
+  __syncthreads();
+  if (tid < 64) {
+    const int lane = tid;
+    int first = nq, last = -1, cnt = 0;
+    bool all_full = true, all_part = true;
+    for (int t0 = 0; t0 < nq; t0 += 64) {
+      const int t = t0 + lane;
+      const int c = t < nq ? (listed ? (int)cls[t] : cg(t)) : 0;
+      const uint64_t m = __ballot(c & 1);
+      if (listed && (c & 1)) {
+        const int pos = cnt + __popcll(m & ((1ull << lane) - 1));
+        act[pos] = (uint16_t)t;
+        acls[pos] = (uint8_t)c;
+      }
+      if (m) {
+        first = min(first, t0 + (int)__builtin_ctzll(m));
+        last = t0 + 63 - (int)__builtin_clzll(m);
+        cnt += __popcll(m);
+      }
+      all_full = all_full && __ballot((c & 1) && !(c & 2)) == 0;
+      all_part = all_part && __ballot((c & 3) == 3) == 0;
+    }
+    if (lane == 0) {
+      hdr[0] = first;
+      hdr[1] = cnt;
+      hdr[2] = all_full ? 3 : all_part ? 1 : -1;
+      hdr[3] = cnt > 0 && last - first + 1 == cnt;
+    }
+  }
+  __syncthreads();
+  QTiles r;
+  r.nq = nq;
+  r.first = __builtin_amdgcn_readfirstlane(hdr[0]);
+  r.cnt = __builtin_amdgcn_readfirstlane(hdr[1]);
+  r.ucls = __builtin_amdgcn_readfirstlane(hdr[2]);
+  r.dense = __builtin_amdgcn_readfirstlane(hdr[3]) != 0;
+  r.listed = listed;
+  r.act = act;
+  r.acls = acls;
+  r.cls = cls;
+  return r;
+}
 // Build-time tuning knob (-D on the compiler line): the wave priority
 // (s_setprio) of the dK/dV waves' critical chains.
 #ifndef DKDV_PRIO
@@ -84,7 +169,8 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
   constexpr int PB_BYTES = 4 * 2 * 2 * 1024;           // [P wave][query block][frag][lane]
   constexpr int PBUF_BYTES = 2 * PB_BYTES;             // two P buffers (alternating tiles)
   __shared__ __attribute__((aligned(16))) char smem[NST * STAGE_BYTES + PBUF_BYTES];
-  __shared__ uint8_t tcls[kMaxBwdTiles];
+  __shared__ uint16_t act[kMaxBwdTiles];
+  __shared__ uint8_t acls[kMaxBwdTiles], tcls[kMaxBwdTiles];
   __shared__ int sched_s[4];
 
   const int vid = xcd_remap(blockIdx.x, p.nbh, p.nkt);
@@ -109,53 +195,13 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
 
   // Query-tile classes (0 = nothing kept for this key block).
   const int nq = (p.Lq + BQ - 1) / BQ;
-  const bool cls_lds = nq <= kMaxBwdTiles;
   auto tclass_g = [&](int t) -> int {
     const int q0 = t * BQ;
     if (CAUSAL && q0 + BQ - 1 < kblk0) return 0;
     if (!p.has_tilemap) return 3;
     return tile_class(p, b, h, q0, q0 + BQ, kblk0, kblk0 + BNK);
   };
-  if (cls_lds)
-    for (int t = tid; t < nq; t += NW * 64) tcls[t] = (uint8_t)tclass_g(t);
-  __syncthreads();
-  auto tclass = [&](int t) -> int {
-    return cls_lds ? __builtin_amdgcn_readfirstlane((int)tcls[t]) : tclass_g(t);
-  };
-  // Summary of the active tiles: when they are one contiguous run with one
-  // class (no mask, key padding, causal) the tile loop needs no lookups.
-  if (wave == 0) {
-    int first = nq, last = -1, cnt = 0;
-    bool all_full = true, all_part = true;
-    for (int t0 = 0; t0 < nq; t0 += 64) {
-      const int t = t0 + lane;
-      const int c = t < nq ? tclass_g(t) : 0;
-      const uint64_t m = __ballot(c & 1);
-      if (m) {
-        first = min(first, t0 + (int)__builtin_ctzll(m));
-        last = t0 + 63 - (int)__builtin_clzll(m);
-        cnt += __popcll(m);
-      }
-      all_full = all_full && __ballot((c & 1) && !(c & 2)) == 0;
-      all_part = all_part && __ballot((c & 3) == 3) == 0;
-    }
-    if (lane == 0) {
-      sched_s[0] = first;
-      sched_s[1] = cnt > 0 && last - first + 1 == cnt;
-      sched_s[2] = all_full ? 3 : all_part ? 1 : -1;
-      sched_s[3] = last;
-    }
-  }
-  __syncthreads();
-  const int t_first = __builtin_amdgcn_readfirstlane(sched_s[0]);
-  const bool dense = __builtin_amdgcn_readfirstlane(sched_s[1]) != 0;
-  const int ucls = __builtin_amdgcn_readfirstlane(sched_s[2]);
-  const int t_last = __builtin_amdgcn_readfirstlane(sched_s[3]);
-  auto next_active = [&](int t) {
-    if (dense) return max(t, t_first) <= t_last ? max(t, t_first) : nq;
-    while (t < nq && !(tclass(t) & 1)) ++t;
-    return t;
-  };
+  const QTiles tl = build_qtiles(act, acls, tcls, sched_s, nq, tid, NW * 64, tclass_g);
 
   // Stationary B operands for this lane's key: K (P wave) or V (dS wave).
   Frag bfr[NC];
@@ -210,7 +256,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
   if constexpr (DBM == kDbFull) {
     if (!pw && kok)
       for (int t = 0; t < nq; ++t)
-        if (!(tclass(t) & 1))
+        if (!tl.active(t, tclass_g))
           for (int i = 0; i < BQ && t * BQ + i < p.Lq; ++i)
             store_db(p, dbbase + (int64_t)(t * BQ + i) * p.dbias_str[2], 0.f);
   }
@@ -375,14 +421,13 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
 
   // P wave, tile t in stage st: P = exp2(S'), published (as T) in P buffer
   // `par`, then dV^T += dO^T P.
-  auto p_tile = [&](int t, int st, int par) NXA_INLINE {
+  auto p_tile = [&](int t, int cls, int st, int par) NXA_INLINE {
     const uint32_t at = lds0 + st * STAGE_BYTES;
     const int q0 = t * BQ;
     __builtin_amdgcn_s_setprio(DKDV_PRIO);  // the exp pass depends on these
     f32x16 x[2], rows[2];
     row_products(at, x, rows, [](int) {});
     __builtin_amdgcn_s_setprio(0);
-    const int cls = ucls >= 0 ? ucls : tclass(t);
     const bool need_mask = mask_rows && !(cls & 2);
     const bool tail = q0 + BQ > p.Lq;
     const bool diag = CAUSAL && (kw0 + 31 > q0);
@@ -468,10 +513,13 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
   // The tile loop is instantiated per role with the same barrier sequence.
   // Iteration i: the P wave handles active tile i, the dS wave tile i - 1
   // (whose P the barrier between them published), and the dS waves copy
-  // tile i + 1 into the stage that tile i - 2 left.
+  // tile i + 1 into the stage that tile i - 2 left.  Tile i + 2 is looked
+  // up one iteration ahead of its use.
   auto run = [&](auto role_tag) {
     constexpr bool PW = decltype(role_tag)::value;
-    int cur = next_active(0), prv = nq;
+    int cur = tl.tile(0, -1, tclass_g), prv = nq;
+    int nxt = cur < nq ? tl.tile(1, cur, tclass_g) : nq;
+    int k = 0;
     int stc = 0, stp = 2, par = 0;
     if constexpr (!PW) {
       const TileSrc s0 = tile_src(cur);
@@ -481,10 +529,10 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
     }
     barrier_nofence();
     while (cur < nq || prv < nq) {
-      const int nxt = cur < nq ? next_active(cur + 1) : nq;
+      const int nn = nxt < nq ? tl.tile(k + 2, nxt, tclass_g) : nq;
       const int stn = stc == 2 ? 0 : stc + 1;
       if constexpr (PW) {
-        if (cur < nq) p_tile(cur, stc, par);
+        if (cur < nq) p_tile(cur, tl.klass(k, cur, tclass_g), stc, par);
         // P is in LDS before the barrier.
         __builtin_amdgcn_s_waitcnt(lgkmcnt_imm(0));
       } else {
@@ -503,6 +551,8 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
       prv = cur;
       stp = stc;
       cur = nxt;
+      nxt = nn;
+      ++k;
       stc = stn;
       par ^= 1;
     }
@@ -584,7 +634,8 @@ __global__ __launch_bounds__(256, 1) void dkdv256_kernel(const Params p) {
   constexpr int ROWS_OFF = 2 * TILE_BYTES;          // -lse2[64], then -delta[64]
   constexpr int STAGE_BYTES = ROWS_OFF + 2 * 64 * 4;
   __shared__ __attribute__((aligned(16))) char smem[NST * STAGE_BYTES];
-  __shared__ uint8_t tcls[kMaxBwdTiles];
+  __shared__ uint16_t act[kMaxBwdTiles];
+  __shared__ uint8_t acls[kMaxBwdTiles], tcls[kMaxBwdTiles];
   __shared__ int sched_s[4];
 
   const int vid = xcd_remap(blockIdx.x, p.nbh, p.nkt);
@@ -608,51 +659,13 @@ __global__ __launch_bounds__(256, 1) void dkdv256_kernel(const Params p) {
 
   // Query-tile classes (0 = nothing kept for this key block), as in dkdv16.
   const int nq = (p.Lq + BQ - 1) / BQ;
-  const bool cls_lds = nq <= kMaxBwdTiles;
   auto tclass_g = [&](int t) -> int {
     const int q0 = t * BQ;
     if (CAUSAL && q0 + BQ - 1 < kblk0) return 0;
     if (!p.has_tilemap) return 3;
     return tile_class(p, b, h, q0, q0 + BQ, kblk0, kblk0 + BNK);
   };
-  if (cls_lds)
-    for (int t = tid; t < nq; t += NW * 64) tcls[t] = (uint8_t)tclass_g(t);
-  __syncthreads();
-  auto tclass = [&](int t) -> int {
-    return cls_lds ? __builtin_amdgcn_readfirstlane((int)tcls[t]) : tclass_g(t);
-  };
-  if (wave == 0) {
-    int first = nq, last = -1, cnt = 0;
-    bool all_full = true, all_part = true;
-    for (int t0 = 0; t0 < nq; t0 += 64) {
-      const int t = t0 + lane;
-      const int c = t < nq ? tclass_g(t) : 0;
-      const uint64_t m = __ballot(c & 1);
-      if (m) {
-        first = min(first, t0 + (int)__builtin_ctzll(m));
-        last = t0 + 63 - (int)__builtin_clzll(m);
-        cnt += __popcll(m);
-      }
-      all_full = all_full && __ballot((c & 1) && !(c & 2)) == 0;
-      all_part = all_part && __ballot((c & 3) == 3) == 0;
-    }
-    if (lane == 0) {
-      sched_s[0] = first;
-      sched_s[1] = cnt > 0 && last - first + 1 == cnt;
-      sched_s[2] = all_full ? 3 : all_part ? 1 : -1;
-      sched_s[3] = last;
-    }
-  }
-  __syncthreads();
-  const int t_first = __builtin_amdgcn_readfirstlane(sched_s[0]);
-  const bool dense = __builtin_amdgcn_readfirstlane(sched_s[1]) != 0;
-  const int ucls = __builtin_amdgcn_readfirstlane(sched_s[2]);
-  const int t_last = __builtin_amdgcn_readfirstlane(sched_s[3]);
-  auto next_active = [&](int t) {
-    if (dense) return max(t, t_first) <= t_last ? max(t, t_first) : nq;
-    while (t < nq && !(tclass(t) & 1)) ++t;
-    return t;
-  };
+  const QTiles tl = build_qtiles(act, acls, tcls, sched_s, nq, tid, NW * 64, tclass_g);
 
   // Stationary B operands of this lane's key: K (for S) and V (for dP).
   Frag kf[NC], vf[NC];
@@ -692,7 +705,7 @@ __global__ __launch_bounds__(256, 1) void dkdv256_kernel(const Params p) {
   if constexpr (DBM == kDbFull) {
     if (kok)
       for (int t = 0; t < nq; ++t)
-        if (!(tclass(t) & 1))
+        if (!tl.active(t, tclass_g))
           for (int i = 0; i < BQ && t * BQ + i < p.Lq; ++i)
             store_db(p, dbbase + (int64_t)(t * BQ + i) * p.dbias_str[2], 0.f);
   }
@@ -766,7 +779,7 @@ __global__ __launch_bounds__(256, 1) void dkdv256_kernel(const Params p) {
   // --- one query tile ------------------------------------------------------------------
   // Tile t in stage st; the copies of a later tile (sources s, stage stn)
   // ride along with the row products.
-  auto tile = [&](int t, int st, const TileSrc& s, int stn) NXA_INLINE {
+  auto tile = [&](int t, int cls, int st, const TileSrc& s, int stn) NXA_INLINE {
     const uint32_t at = lds0 + st * STAGE_BYTES;
     const int q0 = t * BQ;
     copy(s, stn, NCPY);
@@ -816,7 +829,6 @@ __global__ __launch_bounds__(256, 1) void dkdv256_kernel(const Params p) {
     }
 
     // P = exp2(S c - lse2 [+ key term]) in fp32, packed to T for dV.
-    const int cls = ucls >= 0 ? ucls : tclass(t);
     const bool need_mask = mask_rows && !(cls & 2);
     const bool tail = q0 + BQ > p.Lq;
     const bool diag = CAUSAL && (kw0 + 31 > q0);
@@ -901,8 +913,9 @@ __global__ __launch_bounds__(256, 1) void dkdv256_kernel(const Params p) {
   // barrier that ends it, each wave waits for its own copies of the next
   // tile.  Every wave issues the same copies per tile (empty ranges past the
   // last active tile), so the waits are compile-time.
-  int cur = next_active(0);
-  int nxt = cur < nq ? next_active(cur + 1) : nq;
+  int cur = tl.tile(0, -1, tclass_g);
+  int nxt = cur < nq ? tl.tile(1, cur, tclass_g) : nq;
+  int k = 0;
   {
     const TileSrc s0 = tile_src(cur), s1 = tile_src(nxt);
 #pragma unroll
@@ -918,9 +931,9 @@ __global__ __launch_bounds__(256, 1) void dkdv256_kernel(const Params p) {
   barrier_nofence();
   int stc = 0;
   while (cur < nq) {
-    const int nn = nxt < nq ? next_active(nxt + 1) : nq;
+    const int nn = nxt < nq ? tl.tile(k + 2, nxt, tclass_g) : nq;
     const int stn = stc == 0 ? 2 : stc - 1;  // (stc + 2) % 3
-    tile(cur, stc, tile_src(nn), stn);
+    tile(cur, tl.klass(k, cur, tclass_g), stc, tile_src(nn), stn);
     // Tile nxt resident: only the copies of nn may be in flight.
     if (wave < 2)
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(NCPY + 1));
@@ -929,6 +942,7 @@ __global__ __launch_bounds__(256, 1) void dkdv256_kernel(const Params p) {
     barrier_nofence();
     cur = nxt;
     nxt = nn;
+    ++k;
     stc = stc == 2 ? 0 : stc + 1;
   }
   // No copy may still be writing LDS when the block ends.
@@ -999,8 +1013,7 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
   constexpr int NST = DP == 64 ? 3 : 2;                // K / V stages (two blocks per CU)
   constexpr int CPT = 2 * KS::CNT + (ROW_BIAS ? 1 : 0);  // copies per wave per tile
   __shared__ __attribute__((aligned(16))) char smem[NST * STAGE_BYTES];
-  __shared__ uint16_t act[kMaxBwdTiles];  // active key tiles, in order
-  __shared__ uint8_t acls[kMaxBwdTiles];  // their classes
+  __shared__ uint32_t ainfo[kMaxBwdTiles];  // active key tiles, in order: index | class << 16
   __shared__ int nact_s;
 
   const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
@@ -1035,8 +1048,7 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
       const uint64_t m = __ballot(c & 1);
       if (c & 1) {
         const int pos = base + __popcll(m & ((1ull << lane) - 1));
-        act[pos] = (uint16_t)t;
-        acls[pos] = (uint8_t)c;
+        ainfo[pos] = (uint32_t)t | (uint32_t)c << 16;
       }
       base += __popcll(m);
     }
@@ -1044,14 +1056,13 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
   }
   __syncthreads();
   const int n = listed ? __builtin_amdgcn_readfirstlane(nact_s) : nkt;
-  // Contiguous active tiles (no mask, key padding, causal) need no lookup.
-  const bool dense = !listed || n == 0 || act[n - 1] == n - 1;
-  auto tile_of = [&](int i) NXA_INLINE -> int {
-    return dense ? i : __builtin_amdgcn_readfirstlane((int)act[i]);
-  };
-  auto class_of = [&](int i) NXA_INLINE -> int {
-    if (!p.has_tilemap) return 3;
-    return listed ? __builtin_amdgcn_readfirstlane((int)acls[i]) : class_g(tile_of(i));
+  // Active tile i as index | class << 16 (index 0x7fff past the last one).
+  // Listed tiles take one LDS read, which the tile loop issues NST
+  // iterations before the tile's use; unlisted ones are contiguous.
+  auto info_raw = [&](int i) NXA_INLINE -> int {
+    if (i >= n) return 0x7fff;
+    if (listed) return (int)ainfo[i];
+    return i | class_g(i) << 16;
   };
 
   // --- stationary Q^T, dO^T fragments and per-row values ------------------------
@@ -1143,10 +1154,10 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
   struct TileSrc {
     i32x4 k, v, r;  // K rows, V rows, bias row
   };
-  // Sources of active tile i (an empty range past the last one, so every
+  // Sources of key tile kt (an empty range past the last one, so every
   // tile issues the same copies).
-  auto tile_src = [&](int i) NXA_INLINE -> TileSrc {
-    const int k0 = i < n ? tile_of(i) * BN : p.Lk;
+  auto tile_src = [&](int kt) NXA_INLINE -> TileSrc {
+    const int k0 = min(kt * BN, p.Lk);
     // Keys of this tile that exist (0: empty ranges); each range covers only
     // the tile's own rows (below 64 row strides, bounded by the host).
     const int rows = min(p.Lk - k0, BN);
@@ -1204,12 +1215,16 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
   // --- tile loop ----------------------------------------------------------------
   // Tile i lives in stage i % NST; after the barrier that starts tile i the
   // stage of tile i - 1 is free and receives tile i + NST - 1.
+  // win[j]: active tile i + j (info_raw, made uniform).
+  int win[NST];
+#pragma unroll
+  for (int j = 0; j < NST; ++j) win[j] = __builtin_amdgcn_readfirstlane(info_raw(j));
   {
-    TileSrc s0 = tile_src(0);
+    TileSrc s0 = tile_src(win[0] & 0xffff);
 #pragma unroll
     for (int j = 0; j < CPT; ++j) copy(s0, 0, j);
     if constexpr (NST > 2) {
-      TileSrc s1 = tile_src(1);
+      TileSrc s1 = tile_src(win[1] & 0xffff);
 #pragma unroll
       for (int j = 0; j < CPT; ++j) copy(s1, 1, j);
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(CPT));
@@ -1222,11 +1237,12 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
   for (int i = 0; i < n; ++i) {
     const int st = i % NST;
     const int stn = (i + NST - 1) % NST;
-    const TileSrc sn = tile_src(i + NST - 1);
+    const int ahead = info_raw(i + NST);  // uniform after the barrier below
+    const TileSrc sn = tile_src(win[NST - 1] & 0xffff);
     const uint32_t at = lds0 + st * STAGE_BYTES;
-    const int k0 = tile_of(i) * BN;
+    const int k0 = (win[0] & 0xffff) * BN;
 
-    const int cls = class_of(i);
+    const int cls = win[0] >> 16;
     const bool need_mask = p.has_mask && !(cls & 2);
     const bool tail = k0 + BN > p.Lk;
     const bool diag = CAUSAL && (k0 + BN - 1 > qw0);
@@ -1346,6 +1362,9 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
     // flight).
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(CPT * (NST - 2)));
     barrier_nofence();
+#pragma unroll
+    for (int j = 0; j + 1 < NST; ++j) win[j] = win[j + 1];
+    win[NST - 1] = __builtin_amdgcn_readfirstlane(ahead);
   }
   // No copy may still be writing LDS when the block ends.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
