@@ -146,8 +146,7 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   constexpr int KV_COPIES = 2 * KS::CNT + (BMODE == kFbRow ? 1 : 0);
   __shared__ __attribute__((aligned(16))) T ring[NST * STAGE_ELEMS];
   __shared__ __attribute__((aligned(16))) T bring[NSTB * BT_ELEMS];
-  __shared__ uint16_t act[kFwdMaxTiles];  // active key tiles, in order
-  __shared__ uint8_t acls[kFwdMaxTiles];  // their classes
+  __shared__ uint32_t ainfo[kFwdMaxTiles];  // active key tiles, in order: index | class << 16
   __shared__ int nact_s;
 
   const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
@@ -182,8 +181,7 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
       const uint64_t m = __ballot(c & 1);
       if (c & 1) {
         const int pos = base + __popcll(m & ((1ull << lane) - 1));
-        act[pos] = (uint16_t)t;
-        acls[pos] = (uint8_t)c;
+        ainfo[pos] = (uint32_t)t | (uint32_t)c << 16;
       }
       base += __popcll(m);
     }
@@ -191,15 +189,21 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   }
   __syncthreads();
   const int n = listed ? nact_s : nkt;
-  // Contiguous active tiles (no mask, key padding, causal) need no lookup.
-  const bool dense = !listed || n == 0 || act[n - 1] == n - 1;
-  // (LDS reads made wave-uniform: the tile index feeds scalar addresses.)
-  auto tile_of = [&](int i) NXA_INLINE -> int {
-    return dense ? i : __builtin_amdgcn_readfirstlane((int)act[i]);
+  // Active tile i as index | class << 16.  A listed tile takes one LDS
+  // read: the tile loop issues the reads of the next iteration's tiles one
+  // iteration early and makes them wave-uniform (the tile index feeds
+  // scalar addresses) only then, so no lookup waits at a tile's start.
+  // Unlisted tiles are contiguous and computed in place; the tile loop is
+  // instantiated for both (LIST).
+  auto info_raw = [&](int i) NXA_INLINE -> int { return i < n ? (int)ainfo[i] : 0; };
+  auto uni = [](int x) NXA_INLINE -> int { return __builtin_amdgcn_readfirstlane(x); };
+  auto tile_at = [&](auto list_tag, int i, int pre) NXA_INLINE -> int {
+    if constexpr (decltype(list_tag)::value) return pre & 0xffff;
+    else return i;
   };
-  auto class_of = [&](int i) NXA_INLINE -> int {
-    if (!p.has_tilemap) return 3;
-    return listed ? __builtin_amdgcn_readfirstlane((int)acls[i]) : class_g(tile_of(i));
+  auto class_at = [&](auto list_tag, int i, int pre) NXA_INLINE -> int {
+    if constexpr (decltype(list_tag)::value) return pre >> 16;
+    else return class_g(i);
   };
 
   // --- stationary Q^T fragments ----------------------------------------------
@@ -289,8 +293,8 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     }
   }
 
-  auto issue_kv = [&](int i) NXA_INLINE {
-    const int k0 = tile_of(i) * BN;
+  auto issue_kv = [&](int i, int kt) NXA_INLINE {
+    const int k0 = kt * BN;
     const uint32_t at = lds0 + (i % NST) * STAGE_BYTES;
     ksm.issue(kp, ks, k0, p.Lk, p.D, at, wave, lane);
     vsm.issue(vp, vs, k0, p.Lk, p.Dv, at + TILE_BYTES, wave, lane);
@@ -299,9 +303,9 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
       dma4_sv(bp, 2u * (uint32_t)kk, at + 2 * TILE_BYTES + wave * 256);
     }
   };
-  auto issue_bias = [&](int i) NXA_INLINE {
+  auto issue_bias = [&](int i, int kt) NXA_INLINE {
     if constexpr (BMODE == kFbTile) {
-      const int k0 = tile_of(i) * BN;
+      const int k0 = kt * BN;
       const uint32_t bt = ldsb + (i % NSTB) * BT_BYTES + wave * (32 * BN * 2);
       if (k0 + BN <= p.Lk) {
 #pragma unroll
@@ -454,9 +458,9 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   // Whether tile i needs the element-wise pass (mask bytes, key tail, causal
   // diagonal, VALU bias, non-positive scale).  Otherwise the scale is folded
   // into the exponent's FMA and the max is taken on raw scores.
-  auto tile_general = [&](int i) NXA_INLINE -> bool {
-    const int k0 = tile_of(i) * BN;
-    const bool need_mask = p.has_mask && !(class_of(i) & 2);
+  auto tile_general = [&](int kt, int cls) NXA_INLINE -> bool {
+    const int k0 = kt * BN;
+    const bool need_mask = p.has_mask && !(cls & 2);
     const bool tail = k0 + BN > p.Lk;
     const bool diag = CAUSAL && (k0 + BN - 1 > qw0);
     return VALU_BIAS || need_mask || tail || diag || !(p.scale_log2 > 0.f);
@@ -464,9 +468,9 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   // Element-wise pass of a general tile: logits in log2 units, masked
   // entries -inf.  Every element is written exactly once, unconditionally:
   // masked entries are a select, never a divergent partial write.
-  auto mask_tile = [&](int i) NXA_INLINE {
-    const int k0 = tile_of(i) * BN;
-    const bool need_mask = p.has_mask && !(class_of(i) & 2);
+  auto mask_tile = [&](int kt, int cls) NXA_INLINE {
+    const int k0 = kt * BN;
+    const bool need_mask = p.has_mask && !(cls & 2);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -582,18 +586,34 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   };
 
   // --- schedule -------------------------------------------------------------------
-  auto issue_ahead = [&](int i) NXA_INLINE {
-    if (i + AHEAD < n) issue_kv(i + AHEAD);
-    if constexpr (BMODE == kFbTile)
-      if (i + AHEADB < n) issue_bias(i + AHEADB);
+  // Infos an iteration uses, read during the iteration before: the K / V
+  // tile it issues (i + AHEAD), the bias tile (i + AHEADB) and the tile of
+  // its softmax (i, or i - 1 in the lagging waves).
+  struct Infos {
+    int kv, bias, sm;
   };
-  auto prologue = [&]() NXA_INLINE {
+  auto issue_ahead = [&](auto lt, int i, const Infos& f) NXA_INLINE {
+    if (i + AHEAD < n) issue_kv(i + AHEAD, tile_at(lt, i + AHEAD, f.kv));
+    if constexpr (BMODE == kFbTile)
+      if (i + AHEADB < n) issue_bias(i + AHEADB, tile_at(lt, i + AHEADB, f.bias));
+  };
+  auto prologue = [&](auto lt) NXA_INLINE {
     constexpr int NA = AHEAD > AHEADB ? AHEAD : AHEADB;
+    constexpr bool LIST = decltype(lt)::value;
 #pragma unroll
     for (int a = 0; a < NA; ++a) {
-      if (a < AHEAD && a < n) issue_kv(a);
-      if (BMODE == kFbTile && a < AHEADB && a < n) issue_bias(a);
+      const int inf = LIST ? uni(info_raw(a)) : 0;
+      if (a < AHEAD && a < n) issue_kv(a, tile_at(lt, a, inf));
+      if (BMODE == kFbTile && a < AHEADB && a < n) issue_bias(a, tile_at(lt, a, inf));
     }
+  };
+  // Infos of iteration i (sm: tile j), as raw LDS values.
+  auto infos_raw = [&](int i, int j) NXA_INLINE -> Infos {
+    return {info_raw(i + AHEAD), BMODE == kFbTile ? info_raw(i + AHEADB) : 0,
+            info_raw(j < 0 ? 0 : j)};
+  };
+  auto infos_uni = [&](const Infos& r) NXA_INLINE -> Infos {
+    return {uni(r.kv), uni(r.bias), uni(r.sm)};
   };
   // Matrix work of tile i: O += P(i-1) V(i-1), then S = K(i) Q^T.
   auto mfma_phase = [&](int i) NXA_INLINE {
@@ -607,10 +627,11 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   // VALU work of tile i: element-wise pass (general tiles), P = exp(...)
   // and, when needed, the row max and a lazy reference update (O is
   // complete up to tile i-1 here).
-  auto valu_phase = [&](int i) NXA_INLINE {
+  auto valu_phase = [&](auto lt, int i, int pre) NXA_INLINE {
     if (i < 0 || i >= n) return;
-    const bool gen = tile_general(i);
-    if (gen) mask_tile(i);
+    const int kt = tile_at(lt, i, pre), cls = class_at(lt, i, pre);
+    const bool gen = tile_general(kt, cls);
+    if (gen) mask_tile(kt, cls);
     const float cc = gen ? 1.0f : p.scale_log2;
     float alpha;
     // Optimistic pass against the current reference, no row max: kept
@@ -641,43 +662,64 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     // between the phases keeps the pairs in step only with full bias tiles,
     // whose HBM stream it paces (without bias tiles it costs 1-2.5 %).
     constexpr bool MID_BARRIER = BMODE == kFbTile;
-    auto run = [&](auto lag_tag) {
+    auto run = [&](auto lag_tag, auto lt) {
       constexpr bool LAG = decltype(lag_tag)::value;
-      prologue();
+      constexpr bool LIST = decltype(lt)::value;
+      prologue(lt);
+      Infos f = {0, 0, 0};
+      if constexpr (LIST) f = infos_uni(infos_raw(0, LAG ? -1 : 0));
       for (int i = 0; i < n; ++i) {
+        Infos r = {0, 0, 0};
+        if constexpr (LIST) r = infos_raw(i + 1, LAG ? i : i + 1);
         wait_tile(i);
         barrier_nofence();
-        issue_ahead(i);
-        if (LAG) valu_phase(i - 1);
+        issue_ahead(lt, i, f);
+        if (LAG) valu_phase(lt, i - 1, f.sm);
         else mfma_phase(i);
         if constexpr (MID_BARRIER) barrier_nofence();
         if (LAG) mfma_phase(i);
-        else valu_phase(i);
+        else valu_phase(lt, i, f.sm);
+        if constexpr (LIST) f = infos_uni(r);
       }
       if (n > 0) {
         barrier_nofence();
-        if (LAG) valu_phase(n - 1);
+        if (LAG) valu_phase(lt, n - 1, f.sm);
         else mfma_phase(n);
         barrier_nofence();
         if (LAG) mfma_phase(n);
       }
     };
-    if (wave >= NW / 2)
-      run(std::true_type{});
-    else
-      run(std::false_type{});
+    if (wave >= NW / 2) {
+      if (listed) run(std::true_type{}, std::true_type{});
+      else run(std::true_type{}, std::false_type{});
+    } else {
+      if (listed) run(std::false_type{}, std::true_type{});
+      else run(std::false_type{}, std::false_type{});
+    }
   } else {
     // In-step: every wave runs S, softmax, O += P V of tile t between
     // barriers t and t+1.
-    prologue();
-    for (int i = 0; i < n; ++i) {
-      wait_tile(i);
-      barrier_nofence();
-      issue_ahead(i);
-      qk(i);
-      valu_phase(i);
-      pv(i);
-    }
+    auto run = [&](auto lt) {
+      constexpr bool LIST = decltype(lt)::value;
+      prologue(lt);
+      Infos f = {0, 0, 0};
+      if constexpr (LIST) f = infos_uni(infos_raw(0, 0));
+      for (int i = 0; i < n; ++i) {
+        Infos r = {0, 0, 0};
+        if constexpr (LIST) r = infos_raw(i + 1, i + 1);
+        wait_tile(i);
+        barrier_nofence();
+        issue_ahead(lt, i, f);
+        qk(i);
+        valu_phase(lt, i, f.sm);
+        pv(i);
+        if constexpr (LIST) f = infos_uni(r);
+      }
+    };
+    if (listed)
+      run(std::true_type{});
+    else
+      run(std::false_type{});
   }
 
   // Finalise: O = O / l (a fully masked row gives 0/0 = NaN, as the
