@@ -120,6 +120,11 @@ CONFIGS = {
         bwd=True, qk_norm=True,
         workload='bf16 attention fwd+bwd with qk_norm, key-padding mask (C2 with qk-norm)',
     ),
+    'd64': dict(
+        io='bf16', B=8, H=16, L=4096, D=64, bias=None, mask=None, causal=False,
+        bwd=True,
+        workload='bf16 attention fwd+bwd, head dim 64, no mask',
+    ),
     'w256': dict(
         io='bf16', B=4, H=16, L=4096, D=256, bias=None, mask=None, causal=False,
         bwd=True,
