@@ -74,6 +74,15 @@ def _make_mask(rng, kind, B, H, s, t):
         m = rng.random((1, H, 1, t)) < 0.5
         m[..., 0] = True
         return m
+    if kind == 'gaps':
+        # 64-blocks kept with p = 0.3 plus the diagonal, nothing else: the
+        # kept tiles of a row or column of blocks have gaps anywhere,
+        # including before the first, and every query keeps itself.
+        nbq, nbk = -(-s // 64), -(-t // 64)
+        blk = rng.random((nbq, nbk)) < 0.3
+        for i in range(min(nbq, nbk)):
+            blk[i, i] = True
+        return np.kron(blk, np.ones((64, 64), bool))[:s, :t][None, None]
     raise ValueError(kind)
 
 
@@ -330,6 +339,19 @@ def test_bias_bf16_with_f16_io():
 @pytest.mark.parametrize('kind', ['keypad', 'random', 'block', 'rowbcast'])
 def test_masks(dtype, kind):
     _check(dtype, 2, 2, 320, 256, 64, mask_kind=kind, seed=7)
+
+
+@pytest.mark.parametrize('dtype', DTYPES, ids=IDS)
+@pytest.mark.parametrize('d', [64, 128])
+@pytest.mark.parametrize('causal', [False, True], ids=['full', 'causal'])
+def test_block_sparse_tile_lists(dtype, d, causal):
+    """Block-sparse mask over 11 x 11 tiles with gaps before, between and
+    after the kept tiles, with and without causality, and a
+    query-broadcast bias: the kernels walk their lists of active tiles
+    (read an iteration ahead) over runs that are neither contiguous nor of
+    one class."""
+    _check(dtype, 2, 2, 704, 700, d, bias_shape=(1, 2, 1, 700), mask_kind='gaps',
+           causal=causal, seed=40 + d + int(causal))
 
 
 def test_mask_bias_causal_combined():
