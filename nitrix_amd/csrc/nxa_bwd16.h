@@ -33,6 +33,9 @@
 namespace nxa {
 
 constexpr int kMaxBwdTiles = 1024;
+// dQ's packed tile entries: key-tile index in the low 30 bits (and the
+// index past the last active tile), class in the top 2.
+constexpr int kTileEnd = 0x3fffffff;
 
 // Active query tiles of one key block (tile class & 1: something kept).
 // Wave 0 compacts them, in order, into an LDS list, so the tile loop finds
@@ -1013,7 +1016,7 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
   constexpr int NST = DP == 64 ? 3 : 2;                // K / V stages (two blocks per CU)
   constexpr int CPT = 2 * KS::CNT + (ROW_BIAS ? 1 : 0);  // copies per wave per tile
   __shared__ __attribute__((aligned(16))) char smem[NST * STAGE_BYTES];
-  __shared__ uint32_t ainfo[kMaxBwdTiles];  // active key tiles, in order: index | class << 16
+  __shared__ uint32_t ainfo[kMaxBwdTiles];  // active key tiles, in order: index | class << 30
   __shared__ int nact_s;
 
   const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
@@ -1048,7 +1051,7 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
       const uint64_t m = __ballot(c & 1);
       if (c & 1) {
         const int pos = base + __popcll(m & ((1ull << lane) - 1));
-        ainfo[pos] = (uint32_t)t | (uint32_t)c << 16;
+        ainfo[pos] = (uint32_t)t | (uint32_t)c << 30;
       }
       base += __popcll(m);
     }
@@ -1056,13 +1059,15 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
   }
   __syncthreads();
   const int n = listed ? __builtin_amdgcn_readfirstlane(nact_s) : nkt;
-  // Active tile i as index | class << 16 (index 0x7fff past the last one).
+  // Active tile i as index | class << 30 (index kTileEnd past the last
+  // one; a length below 2^31 has fewer than 2^25 key tiles, so any index
+  // fits the 30 bits).
   // Listed tiles take one LDS read, which the tile loop issues NST
   // iterations before the tile's use; unlisted ones are contiguous.
   auto info_raw = [&](int i) NXA_INLINE -> int {
-    if (i >= n) return 0x7fff;
+    if (i >= n) return kTileEnd;
     if (listed) return (int)ainfo[i];
-    return i | class_g(i) << 16;
+    return (int)((uint32_t)i | (uint32_t)class_g(i) << 30);
   };
 
   // --- stationary Q^T, dO^T fragments and per-row values ------------------------
@@ -1157,7 +1162,7 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
   // Sources of key tile kt (an empty range past the last one, so every
   // tile issues the same copies).
   auto tile_src = [&](int kt) NXA_INLINE -> TileSrc {
-    const int k0 = min(kt * BN, p.Lk);
+    const int k0 = (int)min((int64_t)kt * BN, (int64_t)p.Lk);
     // Keys of this tile that exist (0: empty ranges); each range covers only
     // the tile's own rows (below 64 row strides, bounded by the host).
     const int rows = min(p.Lk - k0, BN);
@@ -1220,11 +1225,11 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
 #pragma unroll
   for (int j = 0; j < NST; ++j) win[j] = __builtin_amdgcn_readfirstlane(info_raw(j));
   {
-    TileSrc s0 = tile_src(win[0] & 0xffff);
+    TileSrc s0 = tile_src(win[0] & kTileEnd);
 #pragma unroll
     for (int j = 0; j < CPT; ++j) copy(s0, 0, j);
     if constexpr (NST > 2) {
-      TileSrc s1 = tile_src(win[1] & 0xffff);
+      TileSrc s1 = tile_src(win[1] & kTileEnd);
 #pragma unroll
       for (int j = 0; j < CPT; ++j) copy(s1, 1, j);
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(CPT));
@@ -1238,11 +1243,11 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
     const int st = i % NST;
     const int stn = (i + NST - 1) % NST;
     const int ahead = info_raw(i + NST);  // uniform after the barrier below
-    const TileSrc sn = tile_src(win[NST - 1] & 0xffff);
+    const TileSrc sn = tile_src(win[NST - 1] & kTileEnd);
     const uint32_t at = lds0 + st * STAGE_BYTES;
-    const int k0 = (win[0] & 0xffff) * BN;
+    const int k0 = (win[0] & kTileEnd) * BN;
 
-    const int cls = win[0] >> 16;
+    const int cls = (int)((uint32_t)win[0] >> 30);
     const bool need_mask = p.has_mask && !(cls & 2);
     const bool tail = k0 + BN > p.Lk;
     const bool diag = CAUSAL && (k0 + BN - 1 > qw0);

@@ -308,6 +308,30 @@ def test_block_sparse_more_than_1024_tiles_both_ways():
 
 
 
+def test_more_than_65536_key_tiles():
+    """Lk = 4,194,468 (65,539 key tiles of 64, the last one ragged: more than
+    a 16-bit tile index holds), no mask: the forward and dQ kernels walk the
+    key tiles without a list.  Out and every gradient of the slice against
+    the float64 oracle (8 query rows keep it to seconds)."""
+    B, H, Lq, Lk, D = 1, 1, 8, 65539 * 64 - 28, 64
+    print(f'[case] B{B} H{H} Lq{Lq} Lk{Lk} D{D} no mask, >65536 key tiles', flush=True)
+    gen = torch.Generator(device=_dev())
+    gen.manual_seed(SEED + 9)
+    q = _randn(gen, B, H, Lq, D, grad=True)
+    k, v = (_randn(gen, B, H, Lk, D, grad=True) for _ in range(2))
+    dout = _randn(gen, B, H, Lq, D)
+    out = _fwd_bwd(q, k, v, dout)
+    scale = 1.0 / math.sqrt(D)
+    qn, kn, vn, gn = _np(q), _np(k), _np(v), _np(dout)
+    ref = O.sdpa_forward(qn, kn, vn, scale=scale, acc_dtype=np.float64)
+    dq, dk, dv, _ = O.sdpa_backward(qn, kn, vn, gn, scale=scale, acc_dtype=np.float64)
+    for name, got, want in (('out', out, ref), ('dq', q.grad, dq), ('dk', k.grad, dk),
+                            ('dv', v.grad, dv)):
+        e = _relerr(_np(got), want)
+        print(f'  {name} relerr {e:.2e}', flush=True)
+        assert e <= REL, f'{name} relerr {e:.3e}'
+
+
 # --- head dim 256 ------------------------------------------------------------
 
 
