@@ -144,7 +144,7 @@ __device__ __forceinline__ float load_bias1(const Params& p, int64_t off) {
 // products from registers) and share SIMD w:
 //   * the P wave (w < 4) holds K stationary, forms P = exp2(S c - lse2)
 //     (c = scale * log2(e), one FMA per element on the fp32 scores), publishes
-//     P (as T, in register order) through LDS and accumulates dV^T += dO^T P;
+//     P (in fp16, register order) through LDS and accumulates dV^T += dO^T P;
 //   * the dS wave (w >= 4) holds V stationary and starts at -delta, so its
 //     product is dP - delta; dS = P (dP - delta) with P read back from LDS,
 //     dK^T += Q^T dS (and dbias).
@@ -333,6 +333,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
 
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
   typedef __attribute__((address_space(3))) Frag lds_frag;
+  typedef __attribute__((address_space(3))) f16x8 lds_pfrag;
   typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
   typedef short i16x8 __attribute__((ext_vector_type(8)));
   auto tr_frag = [&](uint32_t a0, uint32_t a1) NXA_INLINE -> Frag {
@@ -463,7 +464,12 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
 #pragma unroll
       for (int f = 0; f < FPB; ++f) {
         pf[qb][f] = M::pack(x[qb], f);
-        *(lds_frag*)(uintptr_t)(poff + par * PB_BYTES + (qb * FPB + f) * 1024) = pf[qb][f];
+        // The exchange carries P in fp16 whatever T is: P <= 1 here, fp16
+        // holds it with more mantissa than bf16, and the dS wave multiplies
+        // it in one mixed-precision FMA.
+        *(lds_pfrag*)(uintptr_t)(poff + par * PB_BYTES + (qb * FPB + f) * 1024) =
+            std::is_same<T, f16>::value ? __builtin_bit_cast(f16x8, pf[qb][f])
+                                        : Mma<f16>::pack(x[qb], f);
       }
     };
     if (general) {
@@ -495,26 +501,22 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
     for (int qb = 0; qb < 2; ++qb) {
 #pragma unroll
       for (int f = 0; f < FPB; ++f) {
-        const Frag pb = *(const lds_frag*)(uintptr_t)(poff + par * PB_BYTES + (qb * FPB + f) * 1024);
+        const f16x8 pb = *(const lds_pfrag*)(uintptr_t)(poff + par * PB_BYTES + (qb * FPB + f) * 1024);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int r = 8 * f + e;
+          // fp16 P times fp32 in one mixed-precision FMA (the half of the
+          // packed pair by op_sel; the conversion is exact, so the result
+          // is that of convert-then-multiply).
+          typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+          const uint32_t pair = __builtin_bit_cast(u32x4, pb)[e >> 1];
           float ds;
-          if constexpr (std::is_same<T, _Float16>::value) {
-            // fp16 P times fp32 in one mixed-precision FMA (the half of the
-            // packed pair by op_sel; the conversion is exact, so the result
-            // is that of convert-then-multiply).
-            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-            const uint32_t pair = __builtin_bit_cast(u32x4, pb)[e >> 1];
-            if (e & 1)
-              asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-                  : "=v"(ds) : "v"(pair), "v"(x[qb][r]));
-            else
-              asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
-                  : "=v"(ds) : "v"(pair), "v"(x[qb][r]));
-          } else {
-            ds = (float)pb[e] * x[qb][r];
-          }
+          if (e & 1)
+            asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                : "=v"(ds) : "v"(pair), "v"(x[qb][r]));
+          else
+            asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
+                : "=v"(ds) : "v"(pair), "v"(x[qb][r]));
           x[qb][r] = ds;
           if constexpr (DBM == kDbFull) {
             const int q = q0 + qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
