@@ -505,18 +505,10 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int r = 8 * f + e;
-          // fp16 P times fp32 in one mixed-precision FMA (the half of the
-          // packed pair by op_sel; the conversion is exact, so the result
-          // is that of convert-then-multiply).
-          typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-          const uint32_t pair = __builtin_bit_cast(u32x4, pb)[e >> 1];
-          float ds;
-          if (e & 1)
-            asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-                : "=v"(ds) : "v"(pair), "v"(x[qb][r]));
-          else
-            asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
-                : "=v"(ds) : "v"(pair), "v"(x[qb][r]));
+          // fp16 P times fp32: an FMA with a zero addend on the converted
+          // half, which the compiler emits as one mixed-precision
+          // v_fma_mix_f32 (exact conversion, one rounding).
+          const float ds = __builtin_fmaf((float)pb[e], x[qb][r], 0.0f);
           x[qb][r] = ds;
           if constexpr (DBM == kDbFull) {
             const int q = q0 + qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);

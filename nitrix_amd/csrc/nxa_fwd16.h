@@ -501,6 +501,11 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     return r;
   };
   auto row_max = [&](float cc) NXA_INLINE -> float {
+    // The max3 below is inline assembly, which the compiler's hazard
+    // checks do not see: on the first tile of a block it can follow the S
+    // products directly, so 16 wait states cover the MFMA result latency
+    // (the rare redo path only).
+    asm volatile("s_nop 7\n\ts_nop 7");
     float mx[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
