@@ -328,7 +328,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
     }
   // Per-row values: rows 8c + 4g .. +3 of each 32-row block.
   const uint32_t rvoff = ROWS_OFF + (pw ? 0 : BQ * 4) + 16 * g;
-  // P exchange: the lane's two T fragments per query block, 1 KB apart.
+  // P exchange: the lane's two fp16 fragments per query block, 1 KB apart.
   const uint32_t poff = pbuf + (wave & 3) * (2 * 2 * 1024) + 16 * lane;
 
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -423,7 +423,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
       }
   };
 
-  // P wave, tile t in stage st: P = exp2(S'), published (as T) in P buffer
+  // P wave, tile t in stage st: P = exp2(S'), published (in fp16) in P buffer
   // `par`, then dV^T += dO^T P.
   auto p_tile = [&](int t, int cls, int st, int par) NXA_INLINE {
     const uint32_t at = lds0 + st * STAGE_BYTES;
