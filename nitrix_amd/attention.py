@@ -180,20 +180,37 @@ def reference_scaled_dot_product_attention(
     scale: Optional[float] = None,
     causal: bool = False,
     qk_norm: bool = False,
+    qk_upcast: Optional[bool] = None,
 ) -> torch.Tensor:
     """Unfused attention, op for op as ``_reference.py:80-181``.
 
     Upcast to ``promote(result_type(q, k, v), float32)``, optional qk-norm,
     ``q k^T``, ``* scale``, ``+ bias``, ``where(mask & causal, ., -inf)``,
     softmax, ``. v``, cast back.  A fully masked row yields NaN.
+
+    ``qk_upcast`` (``docs/feature-requests/attention-no-upcast-knob.md``, the
+    "nitrix determination": a reference-only knob) chooses the precision of
+    the stages instead: ``None`` (default) the above; ``True`` q / k cast to
+    float32, scores and softmax in float32, the probabilities cast back to
+    the I/O dtype and the value product and output in the I/O dtype (the
+    ``upcast_attention=True`` regime); ``False`` every stage in the I/O
+    dtype (``upcast_attention=False``; the caller owns overflow).  For
+    float32 or float64 inputs all three coincide.
     """
     if scale is None:
         scale = default_scale(q.shape[-1])
     out_dtype = torch.promote_types(torch.promote_types(q.dtype, k.dtype), v.dtype)
     acc = torch.promote_types(out_dtype, torch.float32)
-    q = q.to(acc)
-    k = k.to(acc)
-    v = v.to(acc)
+    # Dtypes of the score stage (q k^T, scale, bias, mask, softmax) and of the
+    # value stage (P v).
+    sdt = acc if qk_upcast in (None, True) else out_dtype
+    vdt = acc if qk_upcast is None else out_dtype
+    q = q.to(sdt)
+    k = k.to(sdt)
+    # (a 16-bit value product's right operand is made contiguous: batched
+    # 16-bit products on a transposed view have faulted on gfx950)
+    v = v.to(vdt).contiguous()
+    acc = sdt
     if qk_norm:
         q = qk_rms_norm(q)
         k = qk_rms_norm(k)
@@ -213,7 +230,7 @@ def reference_scaled_dot_product_attention(
             keep.to(torch.bool), logits, torch.full((), -math.inf, dtype=acc, device=logits.device)
         )
     weights = torch.softmax(logits, dim=-1)
-    out = torch.matmul(weights, v)
+    out = torch.matmul(weights.to(vdt), v)
     return out.to(out_dtype)
 
 
@@ -604,6 +621,15 @@ def scaled_dot_product_attention_hip(
     return _SdpaHip.apply(q, k, v, bias, mask, float(scale), bool(causal))
 
 
+def _io_dtype(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.dtype:
+    return torch.promote_types(torch.promote_types(q.dtype, k.dtype), v.dtype)
+
+
+def _below_fp32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+    """Whether the I/O dtype is narrower than float32 (bf16 / fp16)."""
+    return torch.promote_types(_io_dtype(q, k, v), torch.float32) != _io_dtype(q, k, v)
+
+
 def scaled_dot_product_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -614,6 +640,7 @@ def scaled_dot_product_attention(
     scale: Optional[float] = None,
     causal: bool = False,
     qk_norm: bool = False,
+    qk_upcast: Optional[bool] = None,
     backend: str = 'auto',
 ) -> torch.Tensor:
     """Scaled-dot-product attention with backend dispatch
@@ -628,8 +655,28 @@ def scaled_dot_product_attention(
     ``backend``: ``'hip'`` (fused gfx950 kernels), ``'jax'`` (the unfused
     reference engine) or ``'auto'`` (``'hip'`` on a gfx950 device, else
     ``'jax'``; ``NITRIX_BACKEND`` and reproducible mode as in the reference).
+
+    ``qk_upcast`` (default ``None``) selects the reference engine's stage
+    precisions (:func:`reference_scaled_dot_product_attention`).  With
+    bf16 / fp16 inputs ``True`` or ``False`` asks for accumulation below
+    float32, which the fused kernels (float32 online softmax) do not
+    provide: ``backend='hip'`` then raises :class:`NitrixBackendError` and
+    ``'auto'`` resolves to the reference engine (``SPEC.md`` tenet 11,
+    corollary (a)).  With float32 / float64 inputs it changes nothing.
     """
     _validate(q, k, v)
+    if qk_upcast is not None and _below_fp32(q, k, v):
+        if backend in ('hip', 'pallas-cuda'):
+            raise NitrixBackendError(
+                f'scaled_dot_product_attention: qk_upcast={qk_upcast!r} with '
+                f'{_io_dtype(q, k, v)} inputs asks for accumulation below float32, '
+                f'which backend={backend!r} (float32 online softmax) does not provide. '
+                "Use backend='jax' or backend='auto'."
+            )
+        return reference_scaled_dot_product_attention(
+            q, k, v, bias=bias, mask=mask, scale=scale, causal=causal,
+            qk_norm=qk_norm, qk_upcast=qk_upcast,
+        )
     resolved_scale = default_scale(q.shape[-1]) if scale is None else scale
     resolved = resolve_backend(backend, q.device)
     if resolved == 'hip':

@@ -13,6 +13,8 @@ an untileable shape falls back loudly to a byte-identical reference output):
   ``NitrixBackendFallback`` and the reference engine's output, byte for
   byte; ``NITRIX_STRICT_BACKEND=1`` turns that into ``NitrixBackendError``;
 * ``qk_norm=False`` is byte-identical to leaving qk_norm out;
+* ``qk_upcast`` with bf16 inputs runs the reference engine under ``auto``
+  and raises under ``hip``; with float32 inputs the fused kernel runs;
 * the peak memory a forward, and a forward + backward, allocate stays below
   one fp32 (s, t) score matrix (``torch.cuda.max_memory_allocated``), and
   the dbias of a bias shared over many (batch, head) pairs needs far less
@@ -86,6 +88,39 @@ def test_auto_dispatch_uses_the_hip_library_without_warning():
     assert _relerr(out.float().cpu().numpy(), ref) <= 2e-2
     hip = scaled_dot_product_attention(q, k, v, backend='hip')
     assert torch.equal(out, hip)
+
+
+@pytest.mark.parametrize('up', [True, False])
+def test_qk_upcast_dispatch_on_the_device(up):
+    """bf16 with ``qk_upcast`` set asks for sub-float32 accumulation: ``auto``
+    runs the reference engine (no fused launch, no warning, the reference's
+    bits) and ``hip`` raises; with float32 inputs the knob changes nothing
+    and ``hip`` runs the fused kernel."""
+    from nitrix_amd import _lib
+    from nitrix_amd import reference_scaled_dot_product_attention as ref_sdpa
+
+    print(f'[case] qk_upcast={up} dispatch', flush=True)
+    q, k, v = (_rand((2, 2, 96, 64), torch.bfloat16, s) for s in (31, 32, 33))
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    try:
+        with warnings.catch_warnings(record=True) as rec:
+            warnings.simplefilter('always')
+            out = scaled_dot_product_attention(q, k, v, qk_upcast=up, backend='auto')
+        torch.cuda.synchronize()
+        _, launches = _lib.profile_read('fwd')
+    finally:
+        _lib.profile_enable(False)
+        _lib.profile_reset()
+    assert not _fallbacks(rec)
+    assert launches == 0, 'a sub-float32 request ran the fused forward'
+    assert torch.equal(out, ref_sdpa(q, k, v, qk_upcast=up))
+    with pytest.raises(NitrixBackendError, match='below float32'):
+        scaled_dot_product_attention(q, k, v, qk_upcast=up, backend='hip')
+    qf, kf, vf = (x.float() for x in (q, k, v))
+    fused = scaled_dot_product_attention(qf, kf, vf, qk_upcast=up, backend='hip')
+    want = O.sdpa_forward(*(x.cpu().numpy() for x in (qf, kf, vf)), acc_dtype=np.float64)
+    assert _relerr(fused.cpu().numpy(), want) <= 1e-5
 
 
 UNTILEABLE = {
