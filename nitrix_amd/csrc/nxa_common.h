@@ -405,6 +405,13 @@ __device__ __forceinline__ void dma16_sv(const void* base, uint32_t voff, uint32
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :: "v"(voff), "s"(base), "s"(m) : "m0");
 }
+// The same, marked non-temporal: for streams read exactly once (full bias
+// tiles), so that they do not displace the reused K / V tiles in the caches.
+__device__ __forceinline__ void dma16_sv_nt(const void* base, uint32_t voff, uint32_t lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+               :: "v"(voff), "s"(base), "s"(m) : "m0");
+}
 __device__ __forceinline__ void dma4_sv(const void* base, uint32_t voff, uint32_t lds) {
   const uint32_t m = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"

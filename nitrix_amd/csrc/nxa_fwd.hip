@@ -45,7 +45,8 @@ __global__ __launch_bounds__(256) void tilemap_kernel(const Params p, int MB,
       if (r < nrows) {
         const uint8_t* m = m0 + (int64_t)r * p.mask_str[2];
         if (vec16 && nc >= 16) {
-          const u32x4 w = *reinterpret_cast<const u32x4*>(m);
+          // (read once: non-temporal)
+          const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(m));
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const uint32_t x = w[i];

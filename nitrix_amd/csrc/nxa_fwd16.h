@@ -309,13 +309,13 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
       const uint32_t bt = ldsb + (i % NSTB) * BT_BYTES + wave * (32 * BN * 2);
       if (k0 + BN <= p.Lk) {
 #pragma unroll
-        for (int m = 0; m < BT_COPIES; ++m) dma16_sv(bp + k0, boff[m], bt + m * 1024);
+        for (int m = 0; m < BT_COPIES; ++m) dma16_sv_nt(bp + k0, boff[m], bt + m * 1024);
       } else {
 #pragma unroll
         for (int m = 0; m < BT_COPIES; ++m) {
           const int ch = bias_chunk(m);
           const int kk = min(k0 + 8 * ch, p.Lk - 8);
-          dma16_sv(bp, boff[m] + 2u * (uint32_t)(kk - 8 * ch), bt + m * 1024);
+          dma16_sv_nt(bp, boff[m] + 2u * (uint32_t)(kk - 8 * ch), bt + m * 1024);
         }
       }
     }
