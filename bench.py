@@ -66,8 +66,8 @@ MEASURED_TRAFFIC = {
     'c1': ('fwd', 2925500),
     'c2': ('dkdv', 903454611),
     'c3': ('dkdv', 1619534130),
-    'c4': ('fwd', 4433131261),
-    'c5': ('dkdv', 817113574),
+    'c4': ('fwd', 4431167414),
+    'c5': ('dkdv', 982554182),
 }
 # VALU instructions (wave64) of the selective scan's backward pass (all five
 # kernels) per step at the ssm configuration, transcendental instructions
