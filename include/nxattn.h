@@ -99,7 +99,10 @@ int nxa_check(const nxa_desc* desc, int has_bias, int has_mask);
 /* Bytes of caller-provided device workspace that nxa_fwd (flags NXA_WS_FWD)
  * or nxa_bwd (NXA_WS_BWD, or NXA_WS_BWD | NXA_WS_DBIAS when dbias is
  * requested) needs for this descriptor: the mask's tile map (one byte per
- * 64 x 64 tile of the mask's own extent), two fp32 values per query row in
+ * 64 x 64 tile of the mask's own extent) and, for 16-bit I/O without causal
+ * masking when the mask varies over queries, the blocks' longest-first
+ * order (three int32 lists per 64 x 64-tile slice, at most 1024 blocks
+ * each; nothing beyond that), two fp32 values per query row in
  * the backward, and for dbias of a bias shared across batch or heads an fp32
  * accumulator of the bias's own extent plus one chunk of per-(batch, head)
  * partials (at most the larger of that accumulator and 256 KiB per query
@@ -111,7 +114,7 @@ size_t nxa_workspace_bytes(const nxa_desc* desc, int has_bias, int has_mask,
 /* Forward: o = softmax(scale * q k^T + bias, masked) v and its lse.
  * bias / mask may be NULL; lse may be NULL.  When mask is given, the first
  * nxa_workspace_bytes(desc, .., 0) bytes of the workspace receive the
- * tile map that nxa_bwd can reuse (tilemap_ready = 1). */
+ * tile map (and block order) that nxa_bwd can reuse (tilemap_ready = 1). */
 int nxa_fwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
             const void* bias, const uint8_t* mask, void* o, float* lse,
             void* workspace, size_t workspace_bytes, void* stream);
@@ -120,10 +123,10 @@ int nxa_fwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
  * the reference: it is for callers that cannot allocate device memory at all
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  The same kernels and results as nxa_fwd; the mask's tile map
- * goes to a static device array of NXA_NOALLOC_SCRATCH_BYTES that every GPU
- * the library runs on holds until the process ends.  A tile map larger than
- * that (nxa_workspace_bytes(desc, .., NXA_WS_FWD)) is NXA_E_WORKSPACE,
- * before any launch.  The scratch keeps the last call's contents and is
+ * (and block order) goes to a static device array of NXA_NOALLOC_SCRATCH_BYTES
+ * that every GPU the library runs on holds until the process ends.  A tile
+ * map larger than that (nxa_workspace_bytes(desc, .., NXA_WS_FWD)) is
+ * NXA_E_WORKSPACE, before any launch.  The scratch keeps the last call's contents and is
  * shared by every call on one GPU: calls that overlap on one GPU (other
  * streams, other threads) race, so the caller serialises them.  Runs on the
  * current device. */
@@ -138,8 +141,9 @@ int nxa_fwd_noalloc(const nxa_desc* desc, const void* q, const void* k,
  * summed, as the reference's _unbroadcast does, in a fixed order.
  * `workspace` must hold nxa_workspace_bytes(desc, .., NXA_WS_BWD, or
  * NXA_WS_BWD | NXA_WS_DBIAS when dbias is non-NULL) bytes; when
- * tilemap_ready is nonzero its leading bytes hold the tile map written by
- * nxa_fwd for the same mask. */
+ * tilemap_ready is nonzero its leading nxa_workspace_bytes(desc, .., 0)
+ * bytes hold the tile map (and block order) written by nxa_fwd for the same
+ * mask. */
 int nxa_bwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
             const void* bias, const uint8_t* mask, const void* o,
             const float* lse, const void* dout, void* dq, void* dk, void* dv,

@@ -178,8 +178,11 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
 
   const int vid = xcd_remap(blockIdx.x, p.nbh, p.nkt);
   const int bh = p.bh0 + vid / p.nkt;
-  const int kt = vid % p.nkt;
   const int b = bh / p.H, h = bh % p.H;
+  // Longest blocks first by the mask's block order (causal: the first key
+  // blocks are the longest and come first in index order).
+  const int kt = p.order ? ordered_tile(p, b, h, p.ord_k128, vid % p.nkt, p.nkt)
+                         : vid % p.nkt;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
   const bool pw = wave < 4;                                   // role (uniform)
@@ -652,8 +655,11 @@ __global__ __launch_bounds__(256, 1) void dkdv256_kernel(const Params p) {
 
   const int vid = xcd_remap(blockIdx.x, p.nbh, p.nkt);
   const int bh = p.bh0 + vid / p.nkt;
-  const int kt = vid % p.nkt;
   const int b = bh / p.H, h = bh % p.H;
+  // Longest blocks first by the mask's block order (causal: the first key
+  // blocks are the longest and come first in index order).
+  const int kt = p.order ? ordered_tile(p, b, h, p.ord_k128, vid % p.nkt, p.nkt)
+                         : vid % p.nkt;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
   const int g = lane >> 5, c32 = lane & 31;
@@ -1030,8 +1036,11 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
 
   const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
   const int bh = vid / p.nqt;
-  const int qt = p.nqt - 1 - (vid % p.nqt);  // longest (causal) blocks first
   const int b = bh / p.H, h = bh % p.H;
+  // Longest blocks first: by the mask's block order, else (causal) the last
+  // query blocks, which see the most keys.
+  const int qt = p.order ? ordered_tile(p, b, h, p.ord_q128, vid % p.nqt, p.nqt)
+                         : p.nqt - 1 - (vid % p.nqt);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
   const int g = lane >> 5, c32 = lane & 31;

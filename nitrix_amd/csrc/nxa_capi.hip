@@ -163,6 +163,11 @@ bool aligned(const void* p, size_t a) {
 struct MaskGeom {
   int MB, MH, MQ, MK, rows;
   size_t bytes;
+  // Block order (nxa::Params::order): per slice nq2 128-row, nq4 256-row and
+  // nk2 128-key blocks; `order` false leaves the blocks in index order.
+  bool order;
+  int nq2, nq4, nk2;
+  size_t order_bytes;
 };
 
 MaskGeom mask_geom(const nxa_desc* d) {
@@ -174,6 +179,16 @@ MaskGeom mask_geom(const nxa_desc* d) {
   m.MQ = qb ? 1 : (d->Lq + nxa::kTile - 1) / nxa::kTile;
   m.MK = (d->Lk + nxa::kTile - 1) / nxa::kTile;
   m.bytes = (size_t)m.MB * m.MH * m.MQ * m.MK;
+  m.nq2 = (m.MQ + 1) / 2;
+  m.nq4 = (m.MQ + 3) / 4;
+  m.nk2 = (m.MK + 1) / 2;
+  // Only a mask that varies over queries gives one head's blocks unequal
+  // work (a broadcast row only switches whole key blocks off); causal calls
+  // keep their own longest-first order; the 16-bit kernels read the order.
+  m.order = !qb && !d->causal && d->io_dtype != NXA_F32 && m.nq2 <= nxa::kOrderMax &&
+            m.nk2 <= nxa::kOrderMax;
+  m.order_bytes =
+      m.order ? (size_t)m.MB * m.MH * (m.nq2 + m.nq4 + m.nk2) * sizeof(int) : 0;
   return m;
 }
 
@@ -214,17 +229,20 @@ DbiasGeom dbias_geom(const nxa_desc* d) {
 }
 
 struct WsLayout {
-  size_t tilemap, delta, acc, partial, total;
+  size_t tilemap, order, delta, acc, partial, total;
 };
 
 // flags: NXA_WS_BWD (bit 0) sizes the backward's per-row values, and
 // NXA_WS_DBIAS (bit 1) its dbias reduction buffers.
 WsLayout ws_layout(const nxa_desc* d, int has_bias, int has_mask, int flags) {
-  WsLayout w{0, 0, 0, 0, 0};
+  WsLayout w{0, 0, 0, 0, 0, 0};
   size_t off = 0;
   if (has_mask) {
+    const MaskGeom m = mask_geom(d);
     w.tilemap = off;
-    off += align256(mask_geom(d).bytes);
+    off += align256(m.bytes);
+    w.order = off;
+    off += align256(m.order_bytes);
   }
   if (flags & NXA_WS_BWD) {
     w.delta = off;  // -delta[B*H*Lq], then -lse2[B*H*Lq]
@@ -343,10 +361,13 @@ nxa::Params base_params(const nxa_desc* d, const void* q, const void* k,
   return p;
 }
 
-// Writes (or just binds) the tile map for `mask` into the workspace.
-int setup_tilemap(nxa::Params& p, const nxa_desc* d, uint8_t* tm, bool build,
+// Writes (or just binds) the tile map for `mask`, and the block order when
+// the mask takes one, into the workspace (`ws` its base).
+int setup_tilemap(nxa::Params& p, const nxa_desc* d, uint8_t* ws, bool build,
                   hipStream_t stream) {
   const MaskGeom m = mask_geom(d);
+  const WsLayout w = ws_layout(d, 0, 1, 0);
+  uint8_t* tm = ws + w.tilemap;
   p.has_tilemap = 1;
   p.tilemap = tm;
   p.tilemap_out = tm;
@@ -355,13 +376,28 @@ int setup_tilemap(nxa::Params& p, const nxa_desc* d, uint8_t* tm, bool build,
   p.tm_str[0] = m.MB > 1 ? (int64_t)m.MH * m.MQ * m.MK : 0;
   p.tm_str[1] = m.MH > 1 ? (int64_t)m.MQ * m.MK : 0;
   p.tm_str[2] = m.MQ > 1 ? m.MK : 0;
+  int* order = reinterpret_cast<int*>(ws + w.order);
+  if (m.order) {
+    const int64_t ps = (int64_t)m.nq2 + m.nq4 + m.nk2;
+    p.order = order;
+    p.ord_str[0] = m.MB > 1 ? m.MH * ps : 0;
+    p.ord_str[1] = m.MH > 1 ? ps : 0;
+    p.ord_q128 = 0;
+    p.ord_q256 = m.nq2;
+    p.ord_k128 = m.nq2 + m.nq4;
+  }
   if (!build) return NXA_OK;
   bool vec16 = aligned(p.mask, 16);
   for (int i = 0; i < 3; ++i) vec16 = vec16 && (p.mask_str[i] % 16 == 0);
   if (m.bytes >= ((size_t)1 << 31))
     return fail(NXA_E_SHAPE, "mask tile map has %zu tiles (limit 2^31)", m.bytes);
-  return launch("tilemap", stream, [&] {
+  int rc = launch("tilemap", stream, [&] {
     nxa::launch_tilemap(p, m.MB, m.MH, m.MQ, m.MK, vec16 ? 1 : 0, stream);
+  });
+  if (rc || !m.order) return rc;
+  const int tm16 = m.MK % 16 == 0 && aligned(tm, 16);
+  return launch("tile_order", stream, [&] {
+    nxa::launch_tile_order(tm, m.MB * m.MH, m.MQ, m.MK, tm16, order, stream);
   });
 }
 
@@ -565,14 +601,12 @@ int run_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
             const void* bias, const uint8_t* mask, void* o, float* lse,
             void* workspace, void* stream_) {
   int rc;
-  const WsLayout ws = ws_layout(d, bias != nullptr, mask != nullptr, 0);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   nxa::Params p = base_params(d, q, k, v, bias, mask);
   p.o = o;
   p.lse = lse;
   if (mask) {
-    rc = setup_tilemap(p, d, static_cast<uint8_t*>(workspace) + ws.tilemap, true,
-                       stream);
+    rc = setup_tilemap(p, d, static_cast<uint8_t*>(workspace), true, stream);
     if (rc) return rc;
   }
   const int dp = padded_dim(d);
@@ -661,7 +695,7 @@ int run_bwd(const nxa_desc* d, const void* q, const void* k, const void* v,
                                [&] { nxa::launch_delta(p, d->io_dtype, stream); })))
     return rc;
   if (mask) {
-    rc = setup_tilemap(p, d, wsb + ws.tilemap, !tilemap_ready, stream);
+    rc = setup_tilemap(p, d, wsb, !tilemap_ready, stream);
     if (rc) return rc;
   }
   DbiasGeom dg{};

@@ -107,7 +107,26 @@ struct Params {
   const void* kraw;
   const float* qrstd;
   const float* krstd;
+  // Block order of a mask that varies over queries (non-causal, 16-bit
+  // kernels): per tile-map slice, the 128-row query blocks, the 256-row
+  // query blocks and the 128-key blocks, each sorted by kept map tiles, most
+  // first (tile_order_kernel).  NULL: blocks in index order.
+  const int* order;
+  int64_t ord_str[2];  // per batch / per head of the slice (0 if broadcast)
+  int ord_q128, ord_q256, ord_k128;  // offsets of the three lists in a slice
 };
+
+// Longest list tile_order_kernel sorts (blocks per list per slice).
+constexpr int kOrderMax = 1024;
+
+// Tile index of the i-th block (of n) of (b, h) under the block order.  The
+// lists are permutations of 0 .. n-1 by construction; the clamp keeps a
+// block inside its head whatever the list holds.
+__device__ __forceinline__ int ordered_tile(const Params& p, int b, int h, int off, int i,
+                                            int n) {
+  const int t = p.order[b * p.ord_str[0] + h * p.ord_str[1] + off + i];
+  return min(max(t, 0), n - 1);
+}
 
 // Gradient of y = x * r (r = rsqrt(mean(x^2) + eps) over one row of n
 // elements) for the row a lane shares with lane ^ 32: dx = r (dy - y

@@ -76,6 +76,114 @@ __global__ __launch_bounds__(256) void tilemap_kernel(const Params p, int MB,
 }
 
 // ---------------------------------------------------------------------------
+// Block order.  The hardware hands out blocks in index order, each CU taking
+// the next one when it is free; when a mask that varies over queries gives
+// the blocks of one head unequal work, the grid ends on whichever blocks
+// come last.  Sorting each head's blocks by their work, most first (the
+// longest-processing-time rule), lets the short ones fill the end.  One
+// workgroup per tile-map slice:
+//  1. work per block, in map tiles: a 128-row block (two map rows) runs one
+//     key tile for every map column either row keeps, a 256-row block (four
+//     rows) likewise, a 128-key block (two map columns) one query tile for
+//     every map row that keeps either column.  Each lane takes four map rows
+//     x 16 map columns; the row counts are summed over the lanes that share
+//     the rows (a segmented shuffle sum, then one LDS add per segment), the
+//     column counts by LDS atomics.
+//  2. position of block i = #{j : c_j > c_i} + #{j < i : c_j = c_i}, a
+//     permutation (ties keep index order).
+// Output per slice: [128-row blocks | 256-row blocks | 128-key blocks].
+// ---------------------------------------------------------------------------
+__device__ void rank_blocks(const int* c, int n, int* out, int tid) {
+  for (int i = tid; i < n; i += 1024) {
+    const int ci = c[i];
+    int r = 0;
+    for (int j = 0; j < n; ++j) {
+      const int cj = c[j];
+      r += (cj > ci) || (cj == ci && j < i);
+    }
+    out[r] = i;
+  }
+}
+
+__global__ __launch_bounds__(1024) void tile_order_kernel(const uint8_t* tm, int MQ, int MK,
+                                                          int vec16, int* order) {
+  __shared__ int cq2[kOrderMax], cq4[kOrderMax / 2], ck2[kOrderMax];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nq2 = (MQ + 1) >> 1, nq4 = (MQ + 3) >> 2, nk2 = (MK + 1) >> 1;
+  for (int i = tid; i < kOrderMax; i += 1024) {
+    cq2[i] = 0;
+    ck2[i] = 0;
+    if (i < kOrderMax / 2) cq4[i] = 0;
+  }
+  __syncthreads();
+  const uint8_t* s = tm + (int64_t)blockIdx.x * MQ * MK;
+  const int nch = (MK + 15) >> 4;  // 16-column chunks per map row
+  const int nitems = nq4 * nch;
+  for (int base = wave * 64; base < nitems; base += 1024) {  // wave-uniform
+    const int it = base + lane;
+    const bool ok = it < nitems;
+    const int g = ok ? it / nch : nq4;  // idle lanes: a row group past the end
+    const int c = ok ? it - g * nch : 0;
+    // bits[r], bit j: map column 16c + j of row 4g + r keeps something.
+    uint32_t bits[4] = {0u, 0u, 0u, 0u};
+    if (ok) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 4 * g + r;
+        if (row < MQ) {
+          const uint8_t* m = s + (int64_t)row * MK + 16 * c;
+          if (vec16) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(m);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) bits[r] |= ((w[i] >> (8 * j)) & 1u) << (4 * i + j);
+          } else {
+            for (int j = 0; j < 16 && 16 * c + j < MK; ++j)
+              bits[r] |= (uint32_t)(m[j] & 1u) << j;
+          }
+        }
+      }
+    }
+    const uint32_t r01 = bits[0] | bits[1], r23 = bits[2] | bits[3];
+    int w01 = __popc(r01), w23 = __popc(r23), w4 = __popc(r01 | r23);
+    // Segmented sums: lanes of one row group are contiguous; after the
+    // doubling steps a lane holds the sum from itself to its segment's end.
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int gd = __shfl_down(g, d);
+      const int a = __shfl_down(w01, d), b = __shfl_down(w23, d), q = __shfl_down(w4, d);
+      if (lane + d < 64 && gd == g) {
+        w01 += a;
+        w23 += b;
+        w4 += q;
+      }
+    }
+    const int gu = __shfl_up(g, 1);
+    if (ok && (lane == 0 || gu != g)) {
+      atomicAdd(&cq2[2 * g], w01);
+      if (2 * g + 1 < nq2) atomicAdd(&cq2[2 * g + 1], w23);
+      atomicAdd(&cq4[g], w4);
+    }
+    if (ok) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int kp = 8 * c + k;
+        int n = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) n += ((bits[r] >> (2 * k)) & 3u) != 0u;
+        if (n && kp < nk2) atomicAdd(&ck2[kp], n);
+      }
+    }
+  }
+  __syncthreads();
+  int* out = order + (int64_t)blockIdx.x * (nq2 + nq4 + nk2);
+  rank_blocks(cq2, nq2, out, tid);
+  rank_blocks(cq4, nq4, out + nq2, tid);
+  rank_blocks(ck2, nk2, out + nq2 + nq4, tid);
+}
+
+// ---------------------------------------------------------------------------
 // Forward kernel for fp32 I/O (16-bit I/O has its own kernel with direct
 // global->LDS tile copies).  Block = 4 waves x 32 queries (128 rows).  Up to
 // DP = 128 two blocks share a CU, so one block's softmax (VALU, v_exp)
@@ -344,6 +452,12 @@ void launch_tilemap(const Params& p, int MB, int MH, int MQ, int MK, int vec16,
   const int n = (int)((pairs + 3) / 4);
   hipLaunchKernelGGL(tilemap_kernel, dim3(n), dim3(256), 0, stream, p, MB, MH,
                      MQ, MK, vec16);
+}
+
+void launch_tile_order(const uint8_t* tilemap, int slices, int MQ, int MK, int vec16,
+                       int* order, hipStream_t stream) {
+  hipLaunchKernelGGL(tile_order_kernel, dim3(slices), dim3(1024), 0, stream, tilemap, MQ,
+                     MK, vec16, order);
 }
 
 template <typename T, int DP, bool HB, bool CA>

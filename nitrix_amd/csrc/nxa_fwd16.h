@@ -151,8 +151,12 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
 
   const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
   const int bh = vid / p.nqt;
-  const int qt = p.nqt - 1 - (vid % p.nqt);  // longest (causal) tiles first
   const int b = bh / p.H, h = bh % p.H;
+  // Longest blocks first: by the mask's block order, else (causal) the last
+  // query tiles, which see the most keys.
+  const int qt = p.order ? ordered_tile(p, b, h, BM == 128 ? p.ord_q128 : p.ord_q256,
+                                        vid % p.nqt, p.nqt)
+                         : p.nqt - 1 - (vid % p.nqt);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
   const int g = lane >> 5, c32 = lane & 31;

@@ -9,6 +9,9 @@ namespace nxa {
 
 void launch_tilemap(const Params& p, int MB, int MH, int MQ, int MK, int vec16,
                     hipStream_t stream);
+// Block order of each tile-map slice (MQ x MK map, slices after one another).
+void launch_tile_order(const uint8_t* tilemap, int slices, int MQ, int MK, int vec16,
+                       int* order, hipStream_t stream);
 void launch_fwd(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_fwd16(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_delta(const Params& p, int io_dtype, hipStream_t stream);

@@ -166,6 +166,40 @@ def test_dbias_workspace_is_bounded_by_the_bias_extent(lib):
     assert lib.nxa_workspace_bytes(ctypes.byref(d), 1, 0, _lib.NXA_WS_BWD | _lib.NXA_WS_DBIAS) == base
 
 
+def _a256(n):
+    return 256 * (-(-n // 256))
+
+
+def test_block_order_workspace(lib):
+    """A mask that varies over queries (16-bit, not causal) adds the block
+    order after the tile map: per mask slice, int32 lists of the 128-row,
+    256-row and 128-key blocks.  Causal calls, fp32 I/O and masks broadcast
+    over queries add nothing."""
+    B, H, Lq, Lk = 2, 3, 1000, 1100
+    MQ, MK = -(-Lq // 64), -(-Lk // 64)
+    lists = -(-MQ // 2) + -(-MQ // 4) + -(-MK // 2)
+    d = _desc(B=B, H=H, Lq=Lq, Lk=Lk)
+    d.mask_str[:] = (0, Lq * Lk, Lk)  # [1, H, Lq, Lk]: H slices
+    fwd = lib.nxa_workspace_bytes(ctypes.byref(d), 0, 1, _lib.NXA_WS_FWD)
+    assert fwd == _a256(H * MQ * MK) + _a256(H * lists * 4)
+    # the backward's per-row values follow the same mask regions
+    rows = _a256(B * H * Lq * 4)
+    assert lib.nxa_workspace_bytes(ctypes.byref(d), 0, 1, _lib.NXA_WS_BWD) == fwd + 2 * rows
+    d.causal = 1
+    assert lib.nxa_workspace_bytes(ctypes.byref(d), 0, 1, _lib.NXA_WS_FWD) == _a256(H * MQ * MK)
+    d = _desc(B=B, H=H, Lq=Lq, Lk=Lk, dtype=_lib.NXA_F32)
+    d.mask_str[:] = (0, Lq * Lk, Lk)
+    assert lib.nxa_workspace_bytes(ctypes.byref(d), 0, 1, _lib.NXA_WS_FWD) == _a256(H * MQ * MK)
+    d = _desc(B=B, H=H, Lq=Lq, Lk=Lk)
+    d.mask_str[:] = (0, Lk, 0)  # [1, H, 1, Lk]
+    assert lib.nxa_workspace_bytes(ctypes.byref(d), 0, 1, _lib.NXA_WS_FWD) == _a256(H * MK)
+    # more than 1024 blocks in a list: blocks stay in index order
+    d = _desc(B=1, H=1, Lq=131072 + 128, Lk=256)
+    d.mask_str[:] = (0, 0, 256)
+    MQ = -(-d.Lq // 64)
+    assert lib.nxa_workspace_bytes(ctypes.byref(d), 0, 1, _lib.NXA_WS_FWD) == _a256(MQ * 4)
+
+
 @pytest.mark.parametrize('which', ['q', 'k', 'v', 'o'])
 def test_row_stride_bound(lib, which):
     """64 rows of a tile are addressed with 32-bit byte offsets: a row stride

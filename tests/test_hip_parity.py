@@ -83,6 +83,15 @@ def _make_mask(rng, kind, B, H, s, t):
         for i in range(min(nbq, nbk)):
             blk[i, i] = True
         return np.kron(blk, np.ones((64, 64), bool))[:s, :t][None, None]
+    if kind == 'blocky':
+        # 64-blocks kept with a density that differs per block row (2-90 %):
+        # the blocks of one head differ widely in work, so the kernels run
+        # them far from index order (longest first).
+        nbq, nbk = -(-s // 64), -(-t // 64)
+        dens = rng.uniform(0.02, 0.9, size=(nbq, 1))
+        blk = rng.random((nbq, nbk)) < dens
+        blk[:, 0] = True
+        return np.kron(blk, np.ones((64, 64), bool))[:s, :t][None, None]
     raise ValueError(kind)
 
 
