@@ -595,7 +595,7 @@ def main() -> int:
     torch.cuda.synchronize()
     _lib.profile_enable(False)
     kernels = {}
-    for kname in ('tilemap', 'fwd', 'delta', 'dkdv', 'dq', 'dbias_reduce',
+    for kname in ('tilemap', 'tile_order', 'fwd', 'delta', 'dkdv', 'dq', 'dbias_reduce',
                   'rms_norm_fwd', 'rms_norm_bwd'):
         tot, n = _lib.profile_read(kname)
         if n:
