@@ -85,102 +85,153 @@ __global__ __launch_bounds__(256) void tilemap_kernel(const Params p, int MB,
 //  1. work per block, in map tiles: a 128-row block (two map rows) runs one
 //     key tile for every map column either row keeps, a 256-row block (four
 //     rows) likewise, a 128-key block (two map columns) one query tile for
-//     every map row that keeps either column.  Each lane takes four map rows
-//     x 16 map columns; the row counts are summed over the lanes that share
-//     the rows (a segmented shuffle sum, then one LDS add per segment), the
-//     column counts by LDS atomics.
+//     every map row that keeps either column.  Each thread keeps one
+//     16-column chunk and walks row groups of four map rows, loading four
+//     groups at a time; a map row stays four words with bit 0 of each byte
+//     (popcounts of ORs give the row counts, packed 16-bit adds the column
+//     counts).  Row counts are summed over the lanes that share the rows (a
+//     segmented shuffle sum, then one LDS add per segment); column counts
+//     stay in registers until one LDS add per column pair.
 //  2. position of block i = #{j : c_j > c_i} + #{j < i : c_j = c_i}, a
-//     permutation (ties keep index order).
+//     permutation (ties keep index order): with key_i = c_i * 2048 +
+//     (2047 - i) it is #{j : key_j > key_i}.  The three lists are ranked at
+//     once, one thread per block, keys read four at a time (entries past a
+//     list's end hold -1, below every key).
 // Output per slice: [128-row blocks | 256-row blocks | 128-key blocks].
 // ---------------------------------------------------------------------------
-__device__ void rank_blocks(const int* c, int n, int* out, int tid) {
-  for (int i = tid; i < n; i += 1024) {
-    const int ci = c[i];
-    int r = 0;
-    for (int j = 0; j < n; ++j) {
-      const int cj = c[j];
-      r += (cj > ci) || (cj == ci && j < i);
-    }
-    out[r] = i;
+__device__ __forceinline__ int rank_of(const int* key, int n, int i) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  const int ki = key[i];
+  int r = 0;
+#pragma unroll 8
+  for (int j = 0; j < n; j += 4) {
+    const i32x4 v = *reinterpret_cast<const i32x4*>(key + j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r += v[e] > ki;
   }
+  return r;
 }
 
 __global__ __launch_bounds__(1024) void tile_order_kernel(const uint8_t* tm, int MQ, int MK,
                                                           int vec16, int* order) {
-  __shared__ int cq2[kOrderMax], cq4[kOrderMax / 2], ck2[kOrderMax];
+  __shared__ __attribute__((aligned(16))) int cq2[kOrderMax];
+  __shared__ __attribute__((aligned(16))) int cq4[kOrderMax / 2];
+  __shared__ __attribute__((aligned(16))) int ck2[kOrderMax];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nq2 = (MQ + 1) >> 1, nq4 = (MQ + 3) >> 2, nk2 = (MK + 1) >> 1;
   for (int i = tid; i < kOrderMax; i += 1024) {
-    cq2[i] = 0;
-    ck2[i] = 0;
-    if (i < kOrderMax / 2) cq4[i] = 0;
+    cq2[i] = i < nq2 ? 0 : -1;
+    ck2[i] = i < nk2 ? 0 : -1;
+    if (i < kOrderMax / 2) cq4[i] = i < nq4 ? 0 : -1;
   }
   __syncthreads();
   const uint8_t* s = tm + (int64_t)blockIdx.x * MQ * MK;
-  const int nch = (MK + 15) >> 4;  // 16-column chunks per map row
-  const int nitems = nq4 * nch;
-  for (int base = wave * 64; base < nitems; base += 1024) {  // wave-uniform
-    const int it = base + lane;
-    const bool ok = it < nitems;
-    const int g = ok ? it / nch : nq4;  // idle lanes: a row group past the end
-    const int c = ok ? it - g * nch : 0;
-    // bits[r], bit j: map column 16c + j of row 4g + r keeps something.
-    uint32_t bits[4] = {0u, 0u, 0u, 0u};
-    if (ok) {
+  // Thread t keeps 16-column chunk c = t % nch and walks the row groups
+  // (four map rows) r0, r0 + tr, ...; lanes of one row group are contiguous.
+  const int nch = (MK + 15) >> 4;  // at most 128 (nk2 <= kOrderMax)
+  const int tr = 1024 / nch;
+  const int c = tid % nch, r0 = tid / nch;
+  const bool live = r0 < tr;
+  const int iters = (nq4 + tr - 1) / tr;  // uniform
+  // Row `row` of the chunk as four words, bit 0 of byte j = map column
+  // 16c + j keeps something (the other bits cleared).
+  auto row_words = [&](int row) -> u32x4 {
+    const uint8_t* m = s + (int64_t)row * MK + 16 * c;
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (vec16) {
+      w = *reinterpret_cast<const u32x4*>(m);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (16 * c + j < MK) w[j >> 2] |= (uint32_t)m[j] << (8 * (j & 3));
+    }
+    return w & 0x01010101u;
+  };
+  // Column-pair counts, two per word: pair 8c + 2i in the low half of
+  // colacc[i], pair 8c + 2i + 1 in the high half (at most MQ each).
+  uint32_t colacc[4] = {0u, 0u, 0u, 0u};
+  constexpr int U = 4;  // row groups whose loads are issued together
+  for (int k0 = 0; k0 < iters; k0 += U) {
+    u32x4 x[U][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int g = r0 + (k0 + u) * tr;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 4 * g + r;
-        if (row < MQ) {
-          const uint8_t* m = s + (int64_t)row * MK + 16 * c;
-          if (vec16) {
-            const u32x4 w = *reinterpret_cast<const u32x4*>(m);
+        x[u][r] = u32x4{0u, 0u, 0u, 0u};
+        if (live && k0 + u < iters && g < nq4 && 4 * g + r < MQ) x[u][r] = row_words(4 * g + r);
+      }
+    }
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+    for (int u = 0; u < U; ++u) {
+      if (k0 + u >= iters) break;  // uniform
+      const int gv = r0 + (k0 + u) * tr;
+      const bool ok = live && gv < nq4;
+      const int g = ok ? gv : nq4 + r0;  // idle lanes: row groups past the end
+      const u32x4 a01 = x[u][0] | x[u][1], a23 = x[u][2] | x[u][3], a4 = a01 | a23;
+      int w01 = 0, w23 = 0, w4 = 0;
 #pragma unroll
-              for (int j = 0; j < 4; ++j) bits[r] |= ((w[i] >> (8 * j)) & 1u) << (4 * i + j);
-          } else {
-            for (int j = 0; j < 16 && 16 * c + j < MK; ++j)
-              bits[r] |= (uint32_t)(m[j] & 1u) << j;
-          }
+      for (int i = 0; i < 4; ++i) {
+        w01 += __popc(a01[i]);
+        w23 += __popc(a23[i]);
+        w4 += __popc(a4[i]);
+      }
+      // Segmented sums: after the doubling steps a lane holds the sum from
+      // itself to the end of its row group's lanes in this wave.
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int gd = __shfl_down(g, d);
+        const int a = __shfl_down(w01, d), b = __shfl_down(w23, d), q = __shfl_down(w4, d);
+        if (lane + d < 64 && gd == g) {
+          w01 += a;
+          w23 += b;
+          w4 += q;
         }
       }
-    }
-    const uint32_t r01 = bits[0] | bits[1], r23 = bits[2] | bits[3];
-    int w01 = __popc(r01), w23 = __popc(r23), w4 = __popc(r01 | r23);
-    // Segmented sums: lanes of one row group are contiguous; after the
-    // doubling steps a lane holds the sum from itself to its segment's end.
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int gd = __shfl_down(g, d);
-      const int a = __shfl_down(w01, d), b = __shfl_down(w23, d), q = __shfl_down(w4, d);
-      if (lane + d < 64 && gd == g) {
-        w01 += a;
-        w23 += b;
-        w4 += q;
+      const int gu = __shfl_up(g, 1);
+      if (ok && (lane == 0 || gu != g)) {
+        atomicAdd(&cq2[2 * g], w01);
+        if (2 * g + 1 < nq2) atomicAdd(&cq2[2 * g + 1], w23);
+        atomicAdd(&cq4[g], w4);
       }
-    }
-    const int gu = __shfl_up(g, 1);
-    if (ok && (lane == 0 || gu != g)) {
-      atomicAdd(&cq2[2 * g], w01);
-      if (2 * g + 1 < nq2) atomicAdd(&cq2[2 * g + 1], w23);
-      atomicAdd(&cq4[g], w4);
-    }
-    if (ok) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int kp = 8 * c + k;
-        int n = 0;
+      for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) n += ((bits[r] >> (2 * k)) & 3u) != 0u;
+        for (int i = 0; i < 4; ++i) colacc[i] += (x[u][r][i] | (x[u][r][i] >> 8)) & 0x00010001u;
+    }
+  }
+  if (live) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kp = 8 * c + 2 * i + h;
+        const int n = (int)((colacc[i] >> (16 * h)) & 0xffffu);
         if (n && kp < nk2) atomicAdd(&ck2[kp], n);
       }
-    }
+  }
+  // Counts -> sort keys count * 2048 + (2047 - index): a larger key sorts
+  // first, equal counts in index order (indices < 2048); entries past the
+  // ends keep -1.
+  __syncthreads();
+  for (int i = tid; i < kOrderMax; i += 1024) {
+    if (i < nq2) cq2[i] = cq2[i] * 2048 + (2047 - i);
+    if (i < nk2) ck2[i] = ck2[i] * 2048 + (2047 - i);
+    if (i < nq4) cq4[i] = cq4[i] * 2048 + (2047 - i);
   }
   __syncthreads();
   int* out = order + (int64_t)blockIdx.x * (nq2 + nq4 + nk2);
-  rank_blocks(cq2, nq2, out, tid);
-  rank_blocks(cq4, nq4, out + nq2, tid);
-  rank_blocks(ck2, nk2, out + nq2 + nq4, tid);
+  for (int u = tid; u < nq2 + nq4 + nk2; u += 1024) {
+    if (u < nq2) {
+      out[rank_of(cq2, nq2, u)] = u;
+    } else if (u < nq2 + nq4) {
+      const int i = u - nq2;
+      out[nq2 + rank_of(cq4, nq4, i)] = i;
+    } else {
+      const int i = u - nq2 - nq4;
+      out[nq2 + nq4 + rank_of(ck2, nk2, i)] = i;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
