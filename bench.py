@@ -67,7 +67,7 @@ MEASURED_TRAFFIC = {
     'c2': ('dkdv', 903454611),
     'c3': ('dkdv', 1619534130),
     'c4': ('fwd', 4431167414),
-    'c5': ('dkdv', 982554182),
+    'c5': ('dkdv', 706384921),
 }
 # VALU instructions (wave64) of the selective scan's backward pass (all five
 # kernels) per step at the ssm configuration, transcendental instructions
