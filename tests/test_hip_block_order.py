@@ -146,3 +146,15 @@ def test_parity_with_block_order(dtype, d, bias):
     B, H, s, t = 1, 2, 1300, 1500
     bias_shape = None if bias is None else (1, H, 1, t)
     _check(dtype, B, H, s, t, d, bias_shape=bias_shape, mask_kind='blocky', seed=11)
+
+
+@pytest.mark.parametrize('d', [64, 128])
+def test_parity_with_per_head_orders(d):
+    """A mask drawn per batch and head (one list per head), with a full bias
+    shared over the batch, so that dbias is summed over it: the dK/dV kernel
+    then runs in chunks of (batch, head) pairs and reads each pair's list
+    (36 key blocks: chunks of ceil(512 / 36) = 15 pairs, so 16 pairs take two
+    launches, the second starting at pair 15)."""
+    B, H, s, t = 8, 2, 200, 4500
+    _check(torch.bfloat16, B, H, s, t, d, bias_shape=(1, H, s, t),
+           mask_kind='blocky_bh', seed=12)

@@ -92,6 +92,13 @@ def _make_mask(rng, kind, B, H, s, t):
         blk = rng.random((nbq, nbk)) < dens
         blk[:, 0] = True
         return np.kron(blk, np.ones((64, 64), bool))[:s, :t][None, None]
+    if kind == 'blocky_bh':
+        # the same, drawn per batch and head: every head has its own order
+        nbq, nbk = -(-s // 64), -(-t // 64)
+        dens = rng.uniform(0.02, 0.9, size=(B, H, nbq, 1))
+        blk = rng.random((B, H, nbq, nbk)) < dens
+        blk[..., 0] = True
+        return np.kron(blk, np.ones((64, 64), bool))[..., :s, :t]
     raise ValueError(kind)
 
 
