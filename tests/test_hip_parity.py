@@ -521,6 +521,17 @@ def test_bitwise_deterministic_reruns(dtype):
         assert torch.equal(x, y), f'{name} differs between identical runs'
 
 
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16], ids=['bf16', 'f16'])
+def test_bitwise_deterministic_reruns_with_block_order(dtype):
+    """The same with a non-causal mask whose block densities differ per row,
+    so the 16-bit kernels run each head's blocks longest first."""
+    print(f'[case] determinism with block order {dtype}', flush=True)
+    a, b = _run_twice(dtype, 4, 2, 1500, 1700, 64, bias_shape=(2, 1500, 1700),
+                      mask_kind='blocky')
+    for name, x, y in zip(('out', 'dq', 'dk', 'dv', 'dbias'), a, b):
+        assert torch.equal(x, y), f'{name} differs between identical runs'
+
+
 def test_in_place_change_before_backward_raises():
     """The inputs are kept with save_for_backward: editing one in place
     between forward and backward raises instead of giving wrong gradients."""
