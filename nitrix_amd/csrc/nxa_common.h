@@ -119,13 +119,14 @@ struct Params {
 // Longest list tile_order_kernel sorts (blocks per list per slice).
 constexpr int kOrderMax = 1024;
 
-// Tile index of the i-th block (of n) of (b, h) under the block order.  The
-// lists are permutations of 0 .. n-1 by construction; the clamp keeps a
-// block inside its head whatever the list holds.
+// Tile index of the i-th block (of n) of (b, h) under the block order, as a
+// block-uniform value.  The lists are permutations of 0 .. n-1 by
+// construction; the clamp keeps a block inside its head whatever the list
+// holds.
 __device__ __forceinline__ int ordered_tile(const Params& p, int b, int h, int off, int i,
                                             int n) {
   const int t = p.order[b * p.ord_str[0] + h * p.ord_str[1] + off + i];
-  return min(max(t, 0), n - 1);
+  return __builtin_amdgcn_readfirstlane(min(max(t, 0), n - 1));
 }
 
 // Gradient of y = x * r (r = rsqrt(mean(x^2) + eps) over one row of n
