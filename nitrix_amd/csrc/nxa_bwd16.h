@@ -1270,6 +1270,10 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
     const bool tail = k0 + BN > p.Lk;
     const bool diag = CAUSAL && (k0 + BN - 1 > qw0);
     const bool general = VALU_BIAS || need_mask || tail || diag;
+    // A tile with nothing but mask bytes to apply: the mask loads read zero
+    // past Lk (the key tail), and query rows past Lq are not stored, as in
+    // the tiles without an element pass.
+    const bool mask_only = !VALU_BIAS && !CAUSAL && need_mask;
     uint32_t ka[NC];
 #pragma unroll
     for (int m = 0; m < NC; ++m) ka[m] = vadd(at, koff[m]);
@@ -1329,16 +1333,18 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
         if (j + PD < NP) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
       }
 
-      // dS^T = P (dP - delta), P = exp2(S c - lse2) (+ element pass).
+      // dS^T = P (dP - delta), P = exp2(S c - lse2) (+ element pass: GEN 1
+      // mask bytes only, GEN 2 everything).
       Frag pd[FPB];
       auto ds_block = [&](auto gen_tag) NXA_INLINE {
-        constexpr bool GEN = decltype(gen_tag)::value;
+        constexpr int GEN = decltype(gen_tag)::value;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int key0 = k0 + kb * 32 + 8 * c + 4 * g;
           f32x4 bv = {0.f, 0.f, 0.f, 0.f};
           uint32_t mw = 0x01010101u;
-          if constexpr (GEN) {
+          if constexpr (GEN == 1) mw = load_mask4(p, mrow + key0, p.Lk - key0);
+          if constexpr (GEN == 2) {
             if constexpr (VALU_BIAS) bv = load_bias4(p, p.bias, brow + key0, p.Lk - key0);
             if (need_mask) mw = load_mask4(p, mrow + key0, p.Lk - key0);
           }
@@ -1346,7 +1352,8 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
           for (int j = 0; j < 4; ++j) {
             const int r = 4 * c + j;
             float x = __builtin_fmaf(s[r], p.scale_log2, neg_lse2);
-            if constexpr (GEN) {
+            if constexpr (GEN == 1) x = mask_bit(mw, j) ? x : -INFINITY;
+            if constexpr (GEN == 2) {
               const int kk = key0 + j;
               if constexpr (VALU_BIAS) x = __builtin_fmaf(bv[j], kLog2e, x);
               bool keep = mask_bit(mw, j) && kk < p.Lk && qok;
@@ -1359,10 +1366,12 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
 #pragma unroll
         for (int f = 0; f < FPB; ++f) pd[f] = M::pack(dp, f);
       };
-      if (general)
-        ds_block(std::true_type{});
+      if (!general)
+        ds_block(std::integral_constant<int, 0>{});
+      else if (mask_only)
+        ds_block(std::integral_constant<int, 1>{});
       else
-        ds_block(std::false_type{});
+        ds_block(std::integral_constant<int, 2>{});
 
       // dQ^T += K^T dS^T.
       constexpr int NQ = FPB * NDB, PQ = NQ < 4 ? NQ : 4;

@@ -469,12 +469,33 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     const bool diag = CAUSAL && (k0 + BN - 1 > qw0);
     return VALU_BIAS || need_mask || tail || diag || !(p.scale_log2 > 0.f);
   };
-  // Element-wise pass of a general tile: logits in log2 units, masked
-  // entries -inf.  Every element is written exactly once, unconditionally:
-  // masked entries are a select, never a divergent partial write.
+  // Whether a general tile needs nothing but its mask bytes (no VALU bias,
+  // not causal, positive scale): its scores then stay raw, masked entries
+  // -inf, and the exponent's FMA applies the scale as on full tiles.  The
+  // mask loads read zero past Lk, so the mask also covers a key tail.
+  auto mask_only = [&](int cls) NXA_INLINE -> bool {
+    return !VALU_BIAS && !CAUSAL && p.has_mask && !(cls & 2) && p.scale_log2 > 0.f;
+  };
+  // Element-wise pass of a general tile: logits in log2 units (raw scores
+  // for mask_only tiles), masked entries -inf.  Every element is written
+  // exactly once, unconditionally: masked entries are a select, never a
+  // divergent partial write.
   auto mask_tile = [&](int kt, int cls) NXA_INLINE {
     const int k0 = kt * BN;
     const bool need_mask = p.has_mask && !(cls & 2);
+    if (mask_only(cls)) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int key0 = k0 + kb * 32 + 8 * c + 4 * g;
+          const uint32_t mw = load_mask4(p, mrow + key0, p.Lk - key0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            S[kb][4 * c + j] = mask_bit(mw, j) ? S[kb][4 * c + j] : -INFINITY;
+        }
+      return;
+    }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -641,7 +662,7 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     const int kt = tile_at(lt, i, pre), cls = class_at(lt, i, pre);
     const bool gen = tile_general(kt, cls);
     if (gen) mask_tile(kt, cls);
-    const float cc = gen ? 1.0f : p.scale_log2;
+    const float cc = gen && !mask_only(cls) ? 1.0f : p.scale_log2;
     float alpha;
     // Optimistic pass against the current reference, no row max: kept
     // when every half-row sum of the tile's P (32 keys) is at most 2^15
