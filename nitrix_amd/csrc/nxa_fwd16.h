@@ -148,6 +148,11 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   __shared__ __attribute__((aligned(16))) T bring[NSTB * BT_ELEMS];
   __shared__ uint32_t ainfo[kFwdMaxTiles];  // active key tiles, in order: index | class << 16
   __shared__ int nact_s;
+  // Mask bytes of the first partial key tiles of a query-broadcast mask
+  // (mstage below): tile index per slot (-1: empty) and 64 bytes per slot.
+  constexpr int kMaskSlots = 4;
+  __shared__ int mslot_kt[kMaskSlots];
+  __shared__ uint32_t mslot_w[kMaskSlots * 16];
 
   const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
   const int bh = vid / p.nqt;
@@ -177,8 +182,17 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   auto class_g = [&](int t) -> int {
     return p.has_tilemap ? tile_class(p, b, h, q0, q0 + BM, t * BN, t * BN + BN) : 3;
   };
+  // A mask shared by every query row (key padding) has the same bytes for
+  // the whole block: wave 0 copies those of the first kMaskSlots partial
+  // tiles into LDS before the first K / V copies, so the element pass of
+  // such a tile reads LDS instead of waiting on a global load (whose wait
+  // would also drain the K / V prefetch).  Loads complete in order, so the
+  // first tile's wait covers the copy and its barrier publishes it.
+  const bool mstage = listed && p.has_mask && p.tm_rows == 1 && p.mask_vec && !VALU_BIAS &&
+                      !CAUSAL && p.scale_log2 > 0.f;
+  const uint8_t* mrow0 = p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] : nullptr;
   if (listed && wave == 0) {
-    int base = 0;
+    int base = 0, nsl = 0;
     for (int t0 = 0; t0 < nkt; t0 += 64) {
       const int t = t0 + lane;
       const int c = t < nkt ? class_g(t) : 0;
@@ -188,8 +202,25 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
         ainfo[pos] = (uint32_t)t | (uint32_t)c << 16;
       }
       base += __popcll(m);
+      if (mstage) {
+        const bool part = (c & 3) == 1;
+        const uint64_t pm = __ballot(part);
+        if (part) {
+          const int s = nsl + __popcll(pm & ((1ull << lane) - 1));
+          if (s < kMaskSlots) mslot_kt[s] = t;
+        }
+        nsl += __popcll(pm);
+      }
     }
     if (lane == 0) nact_s = base;
+    if (mstage) {
+      if (lane >= nsl && lane < kMaskSlots) mslot_kt[lane] = -1;
+      // Lane l: word l % 16 of slot l / 16; bytes past Lk (and empty slots,
+      // addressed past the range) read as zero.
+      const int skt = mslot_kt[lane >> 4];
+      const uint32_t voff = skt >= 0 ? (uint32_t)skt * (uint32_t)BN + 4u * (lane & 15) : 0xfffffff0u;
+      dma4_buf(make_rsrc(mrow0, (uint32_t)p.Lk), voff, lds_offset(mslot_w));
+    }
   }
   __syncthreads();
   const int n = listed ? nact_s : nkt;
@@ -484,6 +515,25 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     const int k0 = kt * BN;
     const bool need_mask = p.has_mask && !(cls & 2);
     if (mask_only(cls)) {
+      int slot = -1;
+      if (mstage) {
+#pragma unroll
+        for (int s = 0; s < kMaskSlots; ++s)
+          if (mslot_kt[s] == kt) slot = s;
+        slot = __builtin_amdgcn_readfirstlane(slot);
+      }
+      if (slot >= 0) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const uint32_t mw = mslot_w[slot * 16 + kb * 8 + 2 * c + g];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              S[kb][4 * c + j] = mask_bit(mw, j) ? S[kb][4 * c + j] : -INFINITY;
+          }
+        return;
+      }
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll

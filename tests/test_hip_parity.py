@@ -522,6 +522,20 @@ def test_bitwise_deterministic_reruns(dtype):
 
 
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16], ids=['bf16', 'f16'])
+@pytest.mark.parametrize('d', [64, 128])
+@pytest.mark.parametrize('kind', ['keypad', 'rowbcast'])
+@pytest.mark.parametrize('t', [1000, 1001])
+def test_query_broadcast_mask_partial_tiles(dtype, d, kind, t):
+    """A mask shared by every query row: the forward copies the mask bytes
+    of a block's first four partial key tiles into LDS (rows of a multiple
+    of four bytes, t = 1000) and reads the rest, or every tile when the rows
+    are not 4-byte aligned (t = 1001), with global loads.  Key padding has
+    one partial tile per batch; the row-broadcast mask (half the keys
+    dropped at random) has every tile partial."""
+    _check(dtype, 3, 2, 300, t, d, mask_kind=kind, seed=31)
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16], ids=['bf16', 'f16'])
 def test_bitwise_deterministic_reruns_with_block_order(dtype):
     """The same with a non-causal mask whose block densities differ per row,
     so the 16-bit kernels run each head's blocks longest first."""
