@@ -126,10 +126,10 @@ int nxa_fwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
  * (and block order) goes to a static device array of NXA_NOALLOC_SCRATCH_BYTES
  * that every GPU the library runs on holds until the process ends.  A tile
  * map larger than that (nxa_workspace_bytes(desc, .., NXA_WS_FWD)) is
- * NXA_E_WORKSPACE, before any launch.  The scratch keeps the last call's contents and is
- * shared by every call on one GPU: calls that overlap on one GPU (other
- * streams, other threads) race, so the caller serialises them.  Runs on the
- * current device. */
+ * NXA_E_WORKSPACE, before any launch.  The scratch keeps the last call's
+ * contents and is shared by every call on one GPU: calls that overlap on one
+ * GPU (other streams, other threads) race, so the caller serialises them.
+ * Runs on the current device. */
 #define NXA_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
 int nxa_fwd_noalloc(const nxa_desc* desc, const void* q, const void* k,
                     const void* v, const void* bias, const uint8_t* mask, void* o,
