@@ -143,7 +143,7 @@ int nxa_fwd_noalloc(const nxa_desc* desc, const void* q, const void* k,
  * NXA_WS_BWD | NXA_WS_DBIAS when dbias is non-NULL) bytes; when
  * tilemap_ready is nonzero its leading nxa_workspace_bytes(desc, .., 0)
  * bytes hold the tile map (and block order) written by nxa_fwd for the same
- * mask. */
+ * descriptor and mask. */
 int nxa_bwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
             const void* bias, const uint8_t* mask, const void* o,
             const float* lse, const void* dout, void* dq, void* dk, void* dv,
