@@ -216,10 +216,15 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     if (mstage) {
       if (lane >= nsl && lane < kMaskSlots) mslot_kt[lane] = -1;
       // Lane l: word l % 16 of slot l / 16; bytes past Lk (and empty slots,
-      // addressed past the range) read as zero.
-      const int skt = mslot_kt[lane >> 4];
-      const uint32_t voff = skt >= 0 ? (uint32_t)skt * (uint32_t)BN + 4u * (lane & 15) : 0xfffffff0u;
-      dma4_buf(make_rsrc(mrow0, (uint32_t)p.Lk), voff, lds_offset(mslot_w));
+      // addressed past the range) read as zero.  Only with a partial tile,
+      // which is an active one: the tile loop then runs and its first wait
+      // covers the copy, so no block ends with it in flight.
+      if (nsl > 0) {
+        const int skt = mslot_kt[lane >> 4];
+        const uint32_t voff =
+            skt >= 0 ? (uint32_t)skt * (uint32_t)BN + 4u * (lane & 15) : 0xfffffff0u;
+        dma4_buf(make_rsrc(mrow0, (uint32_t)p.Lk), voff, lds_offset(mslot_w));
+      }
     }
   }
   __syncthreads();

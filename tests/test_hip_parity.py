@@ -397,6 +397,34 @@ def test_fully_masked_row_is_nan():
     assert relerr(out[ok], ref[ok]) <= 2e-2
 
 
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16], ids=['bf16', 'f16'])
+def test_key_padding_with_an_empty_batch(dtype):
+    """Key padding that keeps no key of one batch (its rows are NaN, as the
+    reference's) beside batches with a partial key tile: the blocks of the
+    empty batch have no active tile at all, so they must end without
+    staging mask bytes."""
+    rng = np.random.default_rng(57)
+    B, H, s, t, d = 3, 2, 200, 1000, 64
+    q = _draw(rng, (B, H, s, d), dtype)
+    k = _draw(rng, (B, H, t, d), dtype)
+    v = _draw(rng, (B, H, t, d), dtype)
+    valid = np.array([700, 0, 1000])
+    mask = (np.arange(t)[None, :] < valid[:, None])[:, None, None, :]
+    from nitrix_amd import scaled_dot_product_attention
+
+    print(f'[case] key padding with an empty batch {dtype}', flush=True)
+    out = scaled_dot_product_attention(
+        _to(q, dtype), _to(k, dtype), _to(v, dtype),
+        mask=torch.from_numpy(mask).to(_dev()), backend='hip',
+    ).float().cpu().numpy()
+    torch.cuda.synchronize()
+    assert np.all(np.isnan(out[1]))
+    ref = O.sdpa_forward(q[[0, 2]], k[[0, 2]], v[[0, 2]], mask=mask[[0, 2]],
+                         acc_dtype=np.float64)
+    assert np.all(np.isfinite(out[[0, 2]]))
+    assert relerr(out[[0, 2]], ref) <= REL[dtype]
+
+
 @pytest.mark.parametrize('name', ATTENTION_CASES)
 def test_reference_golden_fixtures_fp32(name):
     """The reference's own fixtures through the fused fp32 path (d=8, s=6,
