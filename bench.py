@@ -146,9 +146,14 @@ CONFIGS = {
 _ROUND = {'bf16': 'round_bf16', 'f16': 'round_f16'}
 
 
-def _valid_lengths(B, L):
+def _valid_lengths(B, L, round_to=0):
+    """Key-padding valid lengths; `round_to` > 0 rounds each up to a
+    multiple of it (a measurement line: no partial key tile at 64)."""
     rng = np.random.Generator(np.random.PCG64(SEED))
-    return rng.integers(1024, L + 1, size=B)
+    valid = rng.integers(1024, L + 1, size=B)
+    if round_to:
+        valid = np.minimum(L, -(-valid // round_to) * round_to)
+    return valid
 
 
 def _sparse_blocks(L):
@@ -183,7 +188,7 @@ def _cpu_baseline(name, cfg, budget_s: float = 12.0):
     rng = np.random.Generator(np.random.PCG64(SEED + 1))
     scale = 1.0 / math.sqrt(D)
     rows = min(L, 1024)
-    valid = _valid_lengths(B, L) if cfg['mask'] == 'keypad' else None
+    valid = _valid_lengths(B, L, cfg.get('round_lengths', 0)) if cfg['mask'] == 'keypad' else None
     blk = _sparse_blocks(L) if cfg['mask'] == 'blocksparse' else None
     per_pair = 14.0 * D if cfg['bwd'] else 4.0 * D
 
@@ -281,7 +286,7 @@ class Workload:
             self.bias = randn(1, H, 1, L, grad=bwd)
             desc['bias'] = f'[1,{H},1,{L}] {cfg["io"]}' + (' (with dbias)' if bwd else '')
         if cfg['mask'] == 'keypad':
-            valid = _valid_lengths(B, L)
+            valid = _valid_lengths(B, L, cfg.get('round_lengths', 0))
             self.mask = (
                 torch.arange(L, device=dev)[None, :]
                 < torch.as_tensor(valid, device=dev)[:, None]
@@ -525,6 +530,15 @@ def main() -> int:
         help='only run 5 device-to-device copies of MIB MiB (reference '
         'kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)',
     )
+    ap.add_argument(
+        '--round-lengths',
+        type=int,
+        default=0,
+        metavar='N',
+        help='key-padding configurations only: round every valid length up to '
+        'a multiple of N (64: no partial key tile), a measurement line for the '
+        'cost of partial tiles, not a BASELINE configuration',
+    )
     args = ap.parse_args()
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
@@ -558,6 +572,14 @@ def main() -> int:
     torch.cuda.set_device(dev)
     name = args.config
     cfg = CONFIGS[name]
+    if args.round_lengths:
+        if cfg['mask'] != 'keypad' or args.round_lengths < 1:
+            print('--round-lengths needs a key-padding configuration and N >= 1',
+                  file=sys.stderr)
+            return 2
+        cfg = dict(cfg, round_lengths=args.round_lengths,
+                   workload=cfg['workload'] +
+                   f', valid lengths rounded up to multiples of {args.round_lengths}')
     wl = Workload(name, cfg, torch, dev)
     B, H, L, D = cfg['B'], cfg['H'], cfg['L'], cfg['D']
 
