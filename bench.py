@@ -62,6 +62,10 @@ PEAK_HBM_GBS = 8000.0
 # rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled x2 / x1 by a copy-kernel
 # calibration); the passes, the calibration and every kernel's figures are in
 # profiles/attention_hbm_traffic_c1_c5.md.  Reported as roofline.traffic.
+# TRAFFIC_SRC is the fingerprint (_src_fingerprint) of the attention kernel
+# sources the passes ran; when the sources differ, the figure describes other
+# kernels and is reported as stale (traffic null, the old figure beside it).
+TRAFFIC_SRC = None  # measured before fingerprints were recorded: stale
 MEASURED_TRAFFIC = {
     'c1': ('fwd', 2925500),
     'c2': ('dkdv', 903454611),
@@ -75,6 +79,8 @@ MEASURED_TRAFFIC = {
 # rocprofv3 SQ_INSTS_VALU / SQ_INSTS_VALU_TRANS_F32 counts of its kernels in
 # profiles/selective_scan_valu_counters.md.
 SSM_BWD_VALU_WAVE_INSTS = 2.5654e8
+# Fingerprint of nxa_ssm.hip + nxa_common.h when the counts were taken.
+SSM_VALU_SRC = None  # measured before fingerprints were recorded: stale
 SSM_VALU_SOURCE = 'profiles/selective_scan_valu_counters.md (rocprofv3 SQ_INSTS_VALU, SQ_INSTS_VALU_TRANS_F32)'
 PEAK_VALU_TLANEOPS = 256 * 4 * 32 * 2.4e9 / 1e12  # 78.6 T lane-instructions/s
 TRAFFIC_SOURCE = 'profiles/attention_hbm_traffic_c1_c5.md (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1)'
@@ -165,6 +171,32 @@ def _sparse_blocks(L):
     return blk
 
 
+ATTN_SOURCES = ('nxa_common.h', 'nxa_launch.h', 'nxa_fwd16.h', 'nxa_bwd16.h', 'nxa_fwd16.hip',
+                'nxa_fwd16_wide.hip', 'nxa_bwd16.hip', 'nxa_bwd16_wide.hip', 'nxa_fwd.hip',
+                'nxa_bwd.hip', 'nxa_capi.hip', 'nxa_norm.hip')
+SSM_SOURCES = ('nxa_common.h', 'nxa_ssm.hip')
+
+
+def _src_fingerprint(names) -> str:
+    """First 16 hex digits of a sha256 over the named kernel sources
+    (``nitrix_amd/csrc``), names and contents in order."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for n in names:
+        f = os.path.join(_ROOT, 'nitrix_amd', 'csrc', n)
+        h.update(n.encode())
+        h.update(open(f, 'rb').read() if os.path.exists(f) else b'<absent>')
+    return h.hexdigest()[:16]
+
+
+def _host_cores() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1
+
+
 def _blas_threads() -> int:
     try:
         from threadpoolctl import threadpool_info
@@ -242,6 +274,7 @@ def _cpu_baseline(name, cfg, budget_s: float = 12.0):
         'value': flops / dt / 1e12,
         'unit': 'TFLOP/s',
         'cores': int(_blas_threads()),
+        'host_cores': _host_cores(),
         'kind': 'port',
         'sample': (
             f'{n} blocks of {rows} query rows x {L} keys of single (b,h) slices of '
@@ -380,6 +413,7 @@ def _ssm_cpu_baseline(cfg, budget_s: float = 12.0):
         'value': n * L * dm / dt / 1e9,
         'unit': 'Gelem/s',
         'cores': int(_blas_threads()),
+        'host_cores': _host_cores(),
         'kind': 'port',
         'sample': (
             f'{n} slices of 1 x {L} steps x {dm} channels x {N} states of the ssm workload, '
@@ -463,6 +497,7 @@ def _bench_ssm(args, torch) -> int:
     bwd_s = kernels['ssm_bwd']['avg_ms'] * 1e-3
     lane_ops = SSM_BWD_VALU_WAVE_INSTS * 64
     achieved = lane_ops / bwd_s / 1e12
+    src = _src_fingerprint(SSM_SOURCES)
     roofline = {
         'kernel': 'ssm_bwd (backward pass: local, carry, chunk, two reductions)',
         'bound': 'valu',
@@ -472,8 +507,13 @@ def _bench_ssm(args, torch) -> int:
         'frac': round(achieved / PEAK_VALU_TLANEOPS, 4),
         'traffic': None,
         'valu_source': SSM_VALU_SOURCE,
+        'valu_counts_measured_at': SSM_VALU_SRC,
+        'kernel_src': src,
         'compulsory_hbm_gbs': round(bwd_b / bwd_s / 1e9, 2),
     }
+    if src != SSM_VALU_SRC:
+        # The instruction counts were taken on other kernel sources.
+        roofline['valu_counts_stale'] = True
     cpu = None if args.no_cpu_baseline else _ssm_cpu_baseline(cfg)
     line = {
         'metric': f'selective scan fwd+bwd Gelem/s at B{Bn} L{L} D{Dm} N{N} (fp32)',
@@ -512,7 +552,15 @@ def _measured_traffic(name: str, kernel: str) -> dict:
     hit = MEASURED_TRAFFIC.get(name)
     if hit is None or hit[0] != kernel:
         return {}
-    return {'traffic': hit[1], 'traffic_source': TRAFFIC_SOURCE}
+    src = _src_fingerprint(ATTN_SOURCES)
+    out = {'traffic_source': TRAFFIC_SOURCE, 'traffic_measured_at': TRAFFIC_SRC,
+           'kernel_src': src}
+    if src == TRAFFIC_SRC:
+        out['traffic'] = hit[1]
+    else:
+        # Measured on other kernel sources: kept beside, not reported as traffic.
+        out['traffic_stale'] = hit[1]
+    return out
 
 
 def main() -> int:

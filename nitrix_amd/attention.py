@@ -207,8 +207,9 @@ def reference_scaled_dot_product_attention(
     vdt = acc if qk_upcast is None else out_dtype
     q = q.to(sdt)
     k = k.to(sdt)
-    # (a 16-bit value product's right operand is made contiguous: batched
-    # 16-bit products on a transposed view have faulted on gfx950)
+    # (the right operand of every 16-bit product is made contiguous: the
+    # batched bf16 / fp16 products of this PyTorch-ROCm build are documented
+    # to fault the GPU when that operand is a transposed view)
     v = v.to(vdt).contiguous()
     acc = sdt
     if qk_norm:

@@ -186,8 +186,9 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   // the whole block: wave 0 copies those of the first kMaskSlots partial
   // tiles into LDS before the first K / V copies, so the element pass of
   // such a tile reads LDS instead of waiting on a global load (whose wait
-  // would also drain the K / V prefetch).  Loads complete in order, so the
-  // first tile's wait covers the copy and its barrier publishes it.
+  // would also drain the K / V prefetch).  The copy is complete once wave
+  // 0 passes the vmcnt(0) that follows its Q loads (below), and the first
+  // tile barrier publishes it to the other waves.
   const bool mstage = listed && p.has_mask && p.tm_rows == 1 && p.mask_vec && !VALU_BIAS &&
                       !CAUSAL && p.scale_log2 > 0.f;
   const uint8_t* mrow0 = p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] : nullptr;
@@ -216,9 +217,8 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     if (mstage) {
       if (lane >= nsl && lane < kMaskSlots) mslot_kt[lane] = -1;
       // Lane l: word l % 16 of slot l / 16; bytes past Lk (and empty slots,
-      // addressed past the range) read as zero.  Only with a partial tile,
-      // which is an active one: the tile loop then runs and its first wait
-      // covers the copy, so no block ends with it in flight.
+      // addressed past the range) read as zero.  A block without a partial
+      // tile never reads the slots, so it skips the copy.
       if (nsl > 0) {
         const int skt = mslot_kt[lane >> 4];
         const uint32_t voff =
