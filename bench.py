@@ -126,6 +126,11 @@ CONFIGS = {
         bwd=True, qk_norm=True,
         workload='bf16 attention fwd+bwd with qk_norm, key-padding mask (C2 with qk-norm)',
     ),
+    'c2qkf': dict(
+        io='bf16', B=8, H=16, L=4096, D=128, bias=None, mask='keypad', causal=False,
+        bwd=False, qk_norm=True,
+        workload='bf16 attention fwd (no backward) with qk_norm, key-padding mask',
+    ),
     'd64': dict(
         io='bf16', B=8, H=16, L=4096, D=64, bias=None, mask=None, causal=False,
         bwd=True,

@@ -150,6 +150,22 @@ int nxa_bwd(const nxa_desc* desc, const void* q, const void* k, const void* v,
             void* dbias, const int64_t* dbias_str, void* workspace,
             size_t workspace_bytes, int tilemap_ready, void* stream);
 
+/* Forward of attention on RMS-normalised q and k (qk-norm) with q's norm
+ * fused into the kernel.  Replaces, on the fused path, qk_rms_norm(q)
+ * followed by the forward kernel (nn/attention/__init__.py:196-197 with
+ * _reference.py:52-77 and _kernels/cuda/attention.py:768-824): q holds the
+ * raw rows (the descriptor's q strides), k_hat the normalised keys
+ * (nxa_rms_norm_fwd's y); each query block normalises its stationary rows
+ * in registers (y = x * rsqrt(mean(x^2) + eps) in fp32, cast to the I/O
+ * dtype) and, unless they are NULL (a forward without a backward), writes
+ * them to q_hat (q's strides, for the backward) and the per-row rsqrt to
+ * q_rstd ([B, H, Lq] fp32).  Everything else as nxa_fwd.  bf16 / fp16 I/O
+ * with q not broadcast over B or H, else NXA_E_UNSUPPORTED. */
+int nxa_fwd_normed(const nxa_desc* desc, const void* q, const void* k_hat,
+                   const void* v, const void* bias, const uint8_t* mask, void* o,
+                   float* lse, void* q_hat, float* q_rstd, float eps, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
 /* Backward of attention on RMS-normalised q and k (qk-norm) with the norm's
  * VJP fused into the dQ and dK kernels.  Replaces, on the fused path, the
  * autodiff of qk_rms_norm that the reference composes around its kernel
@@ -175,8 +191,9 @@ int nxa_bwd_normed(const nxa_desc* desc, const void* q_hat, const void* k_hat,
  * which the fused path applies in the I/O dtype before the kernel,
  * nn/attention/__init__.py:196-197), with the per-row rsqrt kept in `rstd`
  * (fp32, may be NULL).  Rows of x are x_stride elements apart (unit stride
- * over D); y is [rows, D] contiguous.  D must be a multiple of 8 (bf16,
- * fp16) or 4 (fp32) and the pointers 16-byte aligned.  One pass, HBM-bound. */
+ * over D); y is [rows, D] contiguous.  D must be at most 256 (the fused
+ * attention's head-dim limit) and a multiple of 8 (bf16, fp16) or 4 (fp32),
+ * and the pointers 16-byte aligned.  One pass, HBM-bound. */
 int nxa_rms_norm_fwd(int64_t rows, int32_t D, int32_t dtype, const void* x,
                      int64_t x_stride, void* y, float* rstd, float eps,
                      void* stream);

@@ -52,6 +52,7 @@ EXPORTS = (
     'nxa_workspace_bytes',
     'nxa_fwd',
     'nxa_fwd_noalloc',
+    'nxa_fwd_normed',
     'nxa_bwd',
     'nxa_bwd_normed',
     'nxa_rms_norm_fwd',
@@ -122,6 +123,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.nxa_fwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
     lib.nxa_fwd_noalloc.restype = ctypes.c_int
     lib.nxa_fwd_noalloc.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.nxa_fwd_normed.restype = ctypes.c_int
+    lib.nxa_fwd_normed.argtypes = [
+        dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_float, vp, ctypes.c_size_t, vp,
+    ]
     lib.nxa_bwd.restype = ctypes.c_int
     lib.nxa_bwd.argtypes = [
         dp,

@@ -399,13 +399,15 @@ class _Prepared:
         return torch.empty(nbytes, dtype=torch.uint8, device=self.device)
 
 
-def _forward(prep: _Prepared, for_bwd: bool = False):
+def _forward(prep: _Prepared, for_bwd: bool = False, qnorm=None):
     """Run ``nxa_fwd``; returns ``(o [nb,h,s,d], lse [nb,h,s], workspace)``.
 
     With ``for_bwd`` the workspace is sized for a backward without dbias (it
     starts with the forward's tile map, then the per-row values), so such a
     backward reuses it as is; a backward that wants dbias of a shared bias
-    allocates its larger workspace itself."""
+    allocates its larger workspace itself.  With ``qnorm = (q_hat,
+    q_rstd)`` (``prep.q`` then holds the raw rows) the kernel normalises q
+    itself (``nxa_fwd_normed``) and writes q_hat and its per-row rsqrt."""
     lib = _lib.lib()
     o = torch.empty(
         (prep.nb, prep.h, prep.s, prep.dv), dtype=prep.dtype, device=prep.device
@@ -414,21 +416,14 @@ def _forward(prep: _Prepared, for_bwd: bool = False):
         (prep.nb, prep.h, prep.s), dtype=torch.float32, device=prep.device
     )
     ws = prep.workspace(_lib.NXA_WS_BWD if for_bwd else _lib.NXA_WS_FWD)
-    _lib.check(
-        lib.nxa_fwd(
-            ctypes.byref(prep.desc),
-            _ptr(prep.q),
-            _ptr(prep.k),
-            _ptr(prep.v),
-            _ptr(prep.bias),
-            _ptr(prep.mask),
-            _ptr(o),
-            _ptr(lse),
-            _ptr(ws),
-            0 if ws is None else ws.numel(),
-            prep.stream(),
-        )
-    )
+    args = (ctypes.byref(prep.desc), _ptr(prep.q), _ptr(prep.k), _ptr(prep.v),
+            _ptr(prep.bias), _ptr(prep.mask), _ptr(o), _ptr(lse))
+    tail = (_ptr(ws), 0 if ws is None else ws.numel(), prep.stream())
+    if qnorm is None:
+        _lib.check(lib.nxa_fwd(*args, *tail))
+    else:
+        q_hat, q_rstd = qnorm
+        _lib.check(lib.nxa_fwd_normed(*args, _ptr(q_hat), _ptr(q_rstd), _QK_RMS_EPS, *tail))
     return o, lse, ws
 
 
@@ -567,10 +562,24 @@ class _SdpaNormHip(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, bias, mask, scale, causal):
-        qn, q2, rq = _rms_norm_rows(q)
+        # q is normalised inside the forward kernel (its query blocks hold
+        # the rows stationary), k by the one-pass norm kernel: every query
+        # block streams all key tiles, so normalising them on load would
+        # repeat the work once per query block.
+        # Without a backward the normalised q is not written at all.
+        d = q.shape[-1]
+        q2 = q.reshape(-1, d)
+        if not q2.is_contiguous() or q2.data_ptr() % 16:
+            q2 = q2.contiguous()
+        for_bwd = any(ctx.needs_input_grad[:4])
+        qn = torch.empty_like(q2) if for_bwd else None
+        rq = (torch.empty((q2.shape[0],), dtype=torch.float32, device=q.device)
+              if for_bwd else None)
         kn, k2, rk = _rms_norm_rows(k)
-        prep = _Prepared(qn, kn, v, bias, mask, scale, causal)
-        o, lse, ws = _forward(prep, for_bwd=any(ctx.needs_input_grad[:4]))
+        prep = _Prepared(q2.reshape(q.shape), kn, v, bias, mask, scale, causal)
+        o, lse, ws = _forward(prep, for_bwd=for_bwd, qnorm=(qn, rq))
+        if qn is not None:
+            qn = qn.reshape(q.shape)
         ctx.args = (scale, causal)
         ctx.save_for_backward(
             q, k, v, bias, mask, qn, kn, q2, k2, rq, rk, o, lse,

@@ -530,8 +530,39 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
   // (whose P the barrier between them published), and the dS waves copy
   // tile i + 1 into the stage that tile i - 2 left.  Tile i + 2 is looked
   // up one iteration ahead of its use.
-  auto run = [&](auto role_tag) {
+  // qk-norm: in the last iteration the P waves have no tile; they stage the
+  // raw rows of their keys (and the rows' rsqrt) into the stage that no one
+  // reads then, for the dS waves' norm VJP after the loop, so that no global
+  // load waits at the end of the block.  Rows at [wave % 4][key][DP], the
+  // rsqrt after them.
+  constexpr int KROWS_BYTES = 4 * 32 * DP * 2;
+  static_assert(KROWS_BYTES + 4 * 32 * 4 <= STAGE_BYTES, "staged rows fit one stage");
+  auto stage_krows = [&](int st) NXA_INLINE {
+    // Direct copies (no registers): 1 KB blocks of RPB whole rows; rows past
+    // Lk are outside the range and land as zeros (never read).
+    constexpr int SPR = DP * 2 / 16, RPB = 64 / SPR;
+    const int rows = min(32, p.Lk - kw0);
+    const uint32_t reg = lds0 + st * STAGE_BYTES + (wave & 3) * 32 * DP * 2;
+    const i32x4 rs = make_rsrc((const T*)p.kraw + b * p.k_str[0] + h * p.k_str[1] +
+                                   (int64_t)kw0 * p.k_str[2],
+                               (uint32_t)(max(rows, 0) * p.k_str[2] * 2));
+#pragma unroll
+    for (int m = 0; m < 32 / RPB; ++m) {
+      const int row = m * RPB + lane / SPR;
+      dma16_buf(rs, 2u * (uint32_t)(row * p.k_str[2] + (lane % SPR) * 8), reg + m * 1024);
+    }
+    // The rsqrt of the wave's 32 keys: 4 bytes per lane from lanes 0-31 only
+    // (each wave's 128 bytes sit next to the others').
+    if (lane < 32)
+      dma4_buf(make_rsrc(p.krstd + ((int64_t)b * p.H + h) * p.Lk + kw0,
+                         (uint32_t)(max(rows, 0) * 4)),
+               4u * lane, lds0 + st * STAGE_BYTES + KROWS_BYTES + (wave & 3) * 128);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  };
+  // Returns the stage of the last iteration (-1 when the block had no tile).
+  auto run = [&](auto role_tag) -> int {
     constexpr bool PW = decltype(role_tag)::value;
+    int last = -1;
     int cur = tl.tile(0, -1, tclass_g), prv = nq;
     int nxt = cur < nq ? tl.tile(1, cur, tclass_g) : nq;
     int k = 0;
@@ -548,7 +579,8 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
       const int stn = stc == 2 ? 0 : stc + 1;
       if constexpr (PW) {
         if (cur < nq) p_tile(cur, tl.klass(k, cur, tclass_g), stc, par);
-        // P is in LDS before the barrier.
+        else if (p.qk_norm) stage_krows(stc);
+        // P (or the staged rows) is in LDS before the barrier.
         __builtin_amdgcn_s_waitcnt(lgkmcnt_imm(0));
       } else {
         const TileSrc s = tile_src(nxt);
@@ -563,6 +595,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       }
       barrier_nofence();
+      last = stc;
       prv = cur;
       stp = stc;
       cur = nxt;
@@ -571,24 +604,27 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
       stc = stn;
       par ^= 1;
     }
+    return last;
   };
-  if (pw)
-    run(std::true_type{});
-  else
-    run(std::false_type{});
+  const int last = pw ? run(std::true_type{}) : run(std::false_type{});
   // No copy may still be writing LDS when the block ends.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   if (!pw && p.qk_norm) {
-    // dK of the raw (pre-norm) keys: the norm's VJP on the finished rows.
+    // dK of the raw (pre-norm) keys: the norm's VJP on the finished rows,
+    // whose raw values the P waves staged in the last iteration.
     float gy[NDB][16];
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int e = 0; e < 16; ++e) gy[db][e] = acc[db][e] * p.scale;
-    const int64_t roff = b * p.k_str[0] + h * p.k_str[1] + (int64_t)kc * p.k_str[2];
-    const float r = p.krstd[((int64_t)b * p.H + h) * p.Lk + kc];
-    rms_norm_vjp_rows<T, NDB>(gy, (const T*)p.kraw + roff, r, p.D, g);
+    // A block without an active tile has dK-hat = 0, whose VJP is 0.
+    if (last >= 0) {
+      const T* xl = (const T*)(smem + last * STAGE_BYTES + ((wave & 3) * 32 + c32) * DP * 2);
+      const float r = *reinterpret_cast<const float*>(smem + last * STAGE_BYTES + KROWS_BYTES +
+                                                      ((wave & 3) * 32 + c32) * 4);
+      rms_norm_vjp_rows<T, NDB>(gy, xl, r, p.D, g);
+    }
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -1262,6 +1298,7 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
     const int stn = (i + NST - 1) % NST;
     const int ahead = info_raw(i + NST);  // uniform after the barrier below
     const TileSrc sn = tile_src(win[NST - 1] & kTileEnd);
+    auto copy_next = [&](int j) NXA_INLINE { copy(sn, stn, j); };
     const uint32_t at = lds0 + st * STAGE_BYTES;
     const int k0 = (win[0] & kTileEnd) * BN;
 
@@ -1320,11 +1357,11 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
           M::run(s, abuf[j % PD], qf[m]);
         if (j + PD < NP) abuf[j % PD] = afrag(j + PD);
         const int pc = kb * NP + j;  // product count in this tile
-        if ((pc & 3) == 3 && (pc >> 2) < CPT) copy(sn, stn, pc >> 2);
+        if ((pc & 3) == 3 && (pc >> 2) < CPT) copy_next(pc >> 2);
       }
       if (kb == 1) {
 #pragma unroll
-        for (int jc = NP / 2; jc < CPT; ++jc) copy(sn, stn, jc);
+        for (int jc = NP / 2; jc < CPT; ++jc) copy_next(jc);
       }
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, PD, 0);
 #pragma unroll
@@ -1403,7 +1440,11 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
 
   if (p.qk_norm) {
     // dQ of the raw (pre-norm) queries: the norm's VJP on the finished rows
-    // (both halves of a row take part in the row sum).
+    // (both halves of a row take part in the row sum).  The raw rows are
+    // read here, after the loop: dQ runs two blocks per CU, so the other
+    // block's work covers the wait (staging them in the last iteration
+    // measured no faster and costs the D = 128 kernel registers it has not
+    // got).
     float gy[NDB][16];
 #pragma unroll
     for (int db = 0; db < NDB; ++db)

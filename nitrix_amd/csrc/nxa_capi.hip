@@ -425,6 +425,8 @@ int check_norm(int64_t rows, int32_t D, int32_t dtype, const void* x, int64_t x_
   const int epc = 16 / esize(dtype);
   if (D % epc != 0)
     return fail(NXA_E_UNSUPPORTED, "rms norm: D=%d must be a multiple of %d", D, epc);
+  if (D > 256)
+    return fail(NXA_E_UNSUPPORTED, "rms norm: D=%d exceeds 256 (rows are held in registers)", D);
   if (x_stride < D || x_stride % epc != 0)
     return fail(NXA_E_LAYOUT, "rms norm: row stride %lld must be >= D and a multiple of %d",
                 (long long)x_stride, epc);
@@ -502,9 +504,16 @@ int check_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
   return check_io_ptrs(d, ptrs, names, 4);
 }
 
+// qk-norm of q fused into the forward (nxa_fwd_normed).
+struct FwdNorm {
+  void* q_hat;
+  float* q_rstd;
+  float eps;
+};
+
 int run_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
             const void* bias, const uint8_t* mask, void* o, float* lse,
-            void* workspace, void* stream_);
+            void* workspace, void* stream_, const FwdNorm* fn = nullptr);
 
 // ---------------------------------------------------------------------------
 // Static scratch of nxa_fwd_noalloc: a device array that every GPU the
@@ -575,6 +584,29 @@ int nxa_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
   return run_fwd(d, q, k, v, bias, mask, o, lse, workspace, stream_);
 }
 
+int nxa_fwd_normed(const nxa_desc* d, const void* q, const void* k_hat, const void* v,
+                   const void* bias, const uint8_t* mask, void* o, float* lse,
+                   void* q_hat, float* q_rstd, float eps, void* workspace,
+                   size_t workspace_bytes, void* stream_) {
+  int rc = check_fwd(d, q, k_hat, v, bias, mask, o);
+  if (rc) return rc;
+  if (d->io_dtype != NXA_BF16 && d->io_dtype != NXA_F16)
+    return fail(NXA_E_UNSUPPORTED,
+                "nxa_fwd_normed: bf16 / fp16 I/O only (fp32: nxa_rms_norm_fwd, then nxa_fwd)");
+  if ((d->q_str[0] == 0 && d->B > 1) || (d->q_str[1] == 0 && d->H > 1))
+    return fail(NXA_E_UNSUPPORTED,
+                "nxa_fwd_normed: q broadcast over batch or heads (normalise it with "
+                "nxa_rms_norm_fwd, then nxa_fwd)");
+  if (q_hat && !aligned(q_hat, 16)) return fail(NXA_E_LAYOUT, "q_hat is not 16-byte aligned");
+  if (!(eps >= 0.f)) return fail(NXA_E_ARG, "nxa_fwd_normed: eps must be >= 0");
+  const WsLayout ws = ws_layout(d, bias != nullptr, mask != nullptr, 0);
+  if (ws.total > 0 && (!workspace || workspace_bytes < ws.total))
+    return fail(NXA_E_WORKSPACE, "forward needs %zu workspace bytes, got %zu",
+                ws.total, workspace ? workspace_bytes : (size_t)0);
+  const FwdNorm fn{q_hat, q_rstd, eps};
+  return run_fwd(d, q, k_hat, v, bias, mask, o, lse, workspace, stream_, &fn);
+}
+
 int nxa_fwd_noalloc(const nxa_desc* d, const void* q, const void* k, const void* v,
                     const void* bias, const uint8_t* mask, void* o, float* lse,
                     void* stream_) {
@@ -599,12 +631,18 @@ namespace {
 // mask), then the forward kernel.
 int run_fwd(const nxa_desc* d, const void* q, const void* k, const void* v,
             const void* bias, const uint8_t* mask, void* o, float* lse,
-            void* workspace, void* stream_) {
+            void* workspace, void* stream_, const FwdNorm* fn) {
   int rc;
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   nxa::Params p = base_params(d, q, k, v, bias, mask);
   p.o = o;
   p.lse = lse;
+  if (fn) {
+    p.qn_on = 1;
+    p.qn_out = fn->q_hat;
+    p.qn_rstd = fn->q_rstd;
+    p.qn_eps = fn->eps;
+  }
   if (mask) {
     rc = setup_tilemap(p, d, static_cast<uint8_t*>(workspace), true, stream);
     if (rc) return rc;

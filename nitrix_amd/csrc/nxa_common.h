@@ -107,6 +107,15 @@ struct Params {
   const void* kraw;
   const float* qrstd;
   const float* krstd;
+  // qk-norm of q fused into the 16-bit forward (qn_on): q holds the raw
+  // rows, the kernel normalises its stationary Q fragments (y = x
+  // rsqrt(mean(x^2) + eps), fp32, cast to the I/O dtype) and, where not
+  // NULL, writes them to qn_out (q's strides) and the per-row rsqrt to
+  // qn_rstd ([B, H, Lq]).
+  int qn_on;
+  void* qn_out;
+  float* qn_rstd;
+  float qn_eps;
   // Block order of a mask that varies over queries (non-causal, 16-bit
   // kernels): per tile-map slice, the 128-row query blocks, the 256-row
   // query blocks and the 128-key blocks, each sorted by kept map tiles, most

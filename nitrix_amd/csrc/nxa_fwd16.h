@@ -291,8 +291,40 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   }
 
   // The Q loads complete here, so the waits in the tile loop only count
-  // tile copies.
+  // tile copies (and the normalised rows below, which are older than every
+  // copy: loads complete in order, so waiting for a copy never passes an
+  // older one).
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+  // qk-norm of the raw q row the lane shares with lane ^ 32 (each holds
+  // half of every 16-element chunk; padding past D is zero), in fp32 as the
+  // reference's qk_rms_norm.  The normalised rows the backward streams are
+  // stored here, before the first copies, so that no store is left to
+  // drain when the block ends.
+  if (p.qn_on) {
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int j = 0; j < EPC; ++j) ss = __builtin_fmaf(to_f32(qf[c][j]), to_f32(qf[c][j]), ss);
+    ss += shfl_xor32(ss);
+    const float qn_r = 1.0f / __builtin_sqrtf(ss / (float)p.D + p.qn_eps);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int j = 0; j < EPC; ++j) qf[c][j] = (T)(to_f32(qf[c][j]) * qn_r);
+    if (qok) {
+      if (p.qn_out) {
+        T* qo = (T*)p.qn_out + b * p.q_str[0] + h * p.q_str[1] + (int64_t)qrow * p.q_str[2];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int d = c * KC + g * EPC;
+          if (d < p.D) *reinterpret_cast<Frag*>(qo + d) = qf[c];
+        }
+      }
+      if (p.qn_rstd && g == 0) p.qn_rstd[((int64_t)b * p.H + h) * p.Lq + qrow] = qn_r;
+    }
+  }
 
   f32x16 oacc[NDB];
 #pragma unroll

@@ -8,8 +8,12 @@
 // closed form dx = r (dy - y mean(dy y)) with r = rsqrt(mean(x^2) + eps) and
 // y = x r in fp32 (autodiff through the cast passes the cotangent unchanged).
 //
-// 16 lanes per row, 16-byte loads, fp32 accumulation; the forward keeps r per
-// row for the VJP.  HBM-bound: one read of x (and dy) and one write per pass.
+// 16 lanes per row, 16-byte loads, the whole row held in registers (the
+// head dim is at most 256: two 16-byte chunks per lane for 16-bit types, four
+// for fp32), fp32 accumulation; the forward keeps r per row for the VJP.  A
+// grid of a few blocks per CU strides over the rows, two rows per 16-lane
+// group and step, so each lane has several loads in flight: HBM-bound, one
+// read of x (and dy) and one write per pass.
 #include "nxa_common.h"
 #include "nxa_launch.h"
 
@@ -24,68 +28,120 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
+constexpr int kNormRowsPerStep = 2;  // rows per 16-lane group and loop step
+
+template <typename T>
+struct NormRow {
+  using Frag = typename Mma<T>::Frag;
+  static constexpr int EPC = Mma<T>::EPC;
+  static constexpr int NCH = 256 / (16 * EPC);  // chunks per lane at the largest D
+  Frag v[NCH];
+  __device__ __forceinline__ void load(const T* row, int sub, int D) {
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+      const int c = (k * 16 + sub) * EPC;
+      if (c < D) v[k] = ld16(row + c);
+      else v[k] = zero_frag<T>();
+    }
+  }
+};
+
 template <typename T>
 __global__ __launch_bounds__(256) void rms_norm_fwd_kernel(const NormParams p) {
-  using Frag = typename Mma<T>::Frag;
-  constexpr int EPC = Mma<T>::EPC;
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  using R = NormRow<T>;
+  using Frag = typename R::Frag;
+  constexpr int EPC = R::EPC, NCH = R::NCH, RS = kNormRowsPerStep;
   const int sub = threadIdx.x & 15;
-  if (row >= p.rows) return;  // whole 16-lane groups leave together
-  const T* x = (const T*)p.x + row * p.x_stride;
-  T* y = (T*)p.y + row * p.D;
-  float ss = 0.f;
-  for (int c = sub * EPC; c < p.D; c += 16 * EPC) {
-    const Frag v = ld16(x + c);
+  const int64_t groups = (int64_t)gridDim.x * 16;
+  for (int64_t r0 = ((int64_t)blockIdx.x * 16 + (threadIdx.x >> 4)) * RS; r0 < p.rows;
+       r0 += groups * RS) {
+    R x[RS];
 #pragma unroll
-    for (int j = 0; j < EPC; ++j) ss = __builtin_fmaf(to_f32(v[j]), to_f32(v[j]), ss);
-  }
-  ss = sum16(ss);
-  const float r = 1.0f / __builtin_sqrtf(ss / (float)p.D + p.eps);
-  for (int c = sub * EPC; c < p.D; c += 16 * EPC) {
-    const Frag v = ld16(x + c);
-    Frag o;
+    for (int u = 0; u < RS; ++u)
+      if (r0 + u < p.rows) x[u].load((const T*)p.x + (r0 + u) * p.x_stride, sub, p.D);
 #pragma unroll
-    for (int j = 0; j < EPC; ++j) o[j] = (T)(to_f32(v[j]) * r);
-    *reinterpret_cast<Frag*>(y + c) = o;
+    for (int u = 0; u < RS; ++u) {
+      const int64_t row = r0 + u;
+      if (row >= p.rows) break;  // uniform over the 16-lane group
+      float ss = 0.f;
+#pragma unroll
+      for (int k = 0; k < NCH; ++k)
+#pragma unroll
+        for (int j = 0; j < EPC; ++j)
+          ss = __builtin_fmaf(to_f32(x[u].v[k][j]), to_f32(x[u].v[k][j]), ss);
+      ss = sum16(ss);
+      const float r = 1.0f / __builtin_sqrtf(ss / (float)p.D + p.eps);
+      T* y = (T*)p.y + row * p.D;
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) {
+        const int c = (k * 16 + sub) * EPC;
+        if (c < p.D) {
+          Frag o;
+#pragma unroll
+          for (int j = 0; j < EPC; ++j) o[j] = (T)(to_f32(x[u].v[k][j]) * r);
+          *reinterpret_cast<Frag*>(y + c) = o;
+        }
+      }
+      if (sub == 0 && p.rstd) p.rstd[row] = r;
+    }
   }
-  if (sub == 0 && p.rstd) p.rstd[row] = r;
 }
 
 template <typename T>
 __global__ __launch_bounds__(256) void rms_norm_bwd_kernel(const NormParams p) {
-  using Frag = typename Mma<T>::Frag;
-  constexpr int EPC = Mma<T>::EPC;
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  using R = NormRow<T>;
+  using Frag = typename R::Frag;
+  constexpr int EPC = R::EPC, NCH = R::NCH, RS = kNormRowsPerStep;
   const int sub = threadIdx.x & 15;
-  if (row >= p.rows) return;
-  const T* x = (const T*)p.x + row * p.x_stride;
-  const T* dy = (const T*)p.dy + row * p.D;
-  T* dx = (T*)p.dx + row * p.D;
-  const float r = p.rstd[row];
-  float s = 0.f;  // sum dy * y
-  for (int c = sub * EPC; c < p.D; c += 16 * EPC) {
-    const Frag v = ld16(x + c), g = ld16(dy + c);
+  const int64_t groups = (int64_t)gridDim.x * 16;
+  for (int64_t r0 = ((int64_t)blockIdx.x * 16 + (threadIdx.x >> 4)) * RS; r0 < p.rows;
+       r0 += groups * RS) {
+    R x[RS], gy[RS];
+    float r[RS];
 #pragma unroll
-    for (int j = 0; j < EPC; ++j) s = __builtin_fmaf(to_f32(g[j]), to_f32(v[j]) * r, s);
-  }
-  const float m = sum16(s) / (float)p.D;
-  for (int c = sub * EPC; c < p.D; c += 16 * EPC) {
-    const Frag v = ld16(x + c), g = ld16(dy + c);
-    Frag o;
+    for (int u = 0; u < RS; ++u)
+      if (r0 + u < p.rows) {
+        x[u].load((const T*)p.x + (r0 + u) * p.x_stride, sub, p.D);
+        gy[u].load((const T*)p.dy + (r0 + u) * p.D, sub, p.D);
+        r[u] = p.rstd[r0 + u];
+      }
 #pragma unroll
-    for (int j = 0; j < EPC; ++j)
-      o[j] = (T)(r * (to_f32(g[j]) - to_f32(v[j]) * r * m));
-    *reinterpret_cast<Frag*>(dx + c) = o;
+    for (int u = 0; u < RS; ++u) {
+      const int64_t row = r0 + u;
+      if (row >= p.rows) break;
+      float s = 0.f;  // sum dy * y
+#pragma unroll
+      for (int k = 0; k < NCH; ++k)
+#pragma unroll
+        for (int j = 0; j < EPC; ++j)
+          s = __builtin_fmaf(to_f32(gy[u].v[k][j]), to_f32(x[u].v[k][j]) * r[u], s);
+      const float m = sum16(s) / (float)p.D;
+      T* dx = (T*)p.dx + row * p.D;
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) {
+        const int c = (k * 16 + sub) * EPC;
+        if (c < p.D) {
+          Frag o;
+#pragma unroll
+          for (int j = 0; j < EPC; ++j)
+            o[j] = (T)(r[u] * (to_f32(gy[u].v[k][j]) - to_f32(x[u].v[k][j]) * r[u] * m));
+          *reinterpret_cast<Frag*>(dx + c) = o;
+        }
+      }
+    }
   }
 }
 
 template <typename T>
 static void launch_norm_t(const NormParams& p, bool bwd, hipStream_t stream) {
-  const int64_t blocks = (p.rows + 15) / 16;
+  // Enough 256-thread blocks for eight per CU, fewer for small problems.
+  const int64_t need = (p.rows + 16 * kNormRowsPerStep - 1) / (16 * kNormRowsPerStep);
+  const unsigned blocks = (unsigned)(need < 2048 ? need : 2048);
+  if (blocks == 0) return;
   if (bwd)
-    hipLaunchKernelGGL(rms_norm_bwd_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(rms_norm_bwd_kernel<T>, dim3(blocks), dim3(256), 0, stream, p);
   else
-    hipLaunchKernelGGL(rms_norm_fwd_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(rms_norm_fwd_kernel<T>, dim3(blocks), dim3(256), 0, stream, p);
 }
 
 void launch_rms_norm(const NormParams& p, int dtype, bool bwd, hipStream_t stream) {

@@ -287,3 +287,40 @@ def test_noalloc_forward_rejects_a_tile_map_beyond_the_scratch(lib):
     rc = lib.nxa_fwd_noalloc(ctypes.byref(d), None, ok, ok, None, ok, ok, None, None)
     assert rc == _lib.NXA_E_ARG
 
+
+
+@pytest.mark.parametrize('D, code, text', [
+    (264, _lib.NXA_E_UNSUPPORTED, 'exceeds 256'),
+    (12, _lib.NXA_E_UNSUPPORTED, 'multiple of 8'),
+    (0, _lib.NXA_E_SHAPE, 'D > 0'),
+])
+def test_rms_norm_rejects_head_dims_it_cannot_hold(lib, D, code, text):
+    # Validation happens before any launch, so no GPU is needed.
+    ok = ctypes.c_void_p(0x2000)
+    rc = lib.nxa_rms_norm_fwd(4, D, _lib.NXA_BF16, ok, max(D, 8), ok, None, 1e-6, None)
+    assert rc == code
+    assert text in lib.nxa_last_error().decode()
+    rc = lib.nxa_rms_norm_bwd(4, D, _lib.NXA_BF16, ok, max(D, 8), ok, ok, ok, None)
+    assert rc == code
+
+
+def test_fused_q_norm_forward_rejects_what_it_cannot_take(lib):
+    ok = ctypes.c_void_p(0x2000)
+    d = _desc()
+    d.io_dtype = _lib.NXA_F32
+    rc = lib.nxa_fwd_normed(ctypes.byref(d), ok, ok, ok, None, None, ok, ok, ok, ok, 1e-6,
+                            None, 0, None)
+    assert rc == _lib.NXA_E_UNSUPPORTED and 'bf16 / fp16' in lib.nxa_last_error().decode()
+    d = _desc()
+    d.B, d.q_str[0] = 2, 0
+    rc = lib.nxa_fwd_normed(ctypes.byref(d), ok, ok, ok, None, None, ok, ok, ok, ok, 1e-6,
+                            None, 0, None)
+    assert rc == _lib.NXA_E_UNSUPPORTED and 'broadcast' in lib.nxa_last_error().decode()
+    d = _desc()
+    odd = ctypes.c_void_p(0x1008)
+    rc = lib.nxa_fwd_normed(ctypes.byref(d), ok, ok, ok, None, None, ok, ok, odd, ok, 1e-6,
+                            None, 0, None)
+    assert rc == _lib.NXA_E_LAYOUT and 'q_hat' in lib.nxa_last_error().decode()
+    rc = lib.nxa_fwd_normed(ctypes.byref(d), ok, ok, ok, None, None, ok, ok, ok, ok, -1.0,
+                            None, 0, None)
+    assert rc == _lib.NXA_E_ARG

@@ -143,7 +143,8 @@ def test_fused_qk_norm_backward(name, B, H, s, t, d, dv, kw):
     finally:
         _lib.profile_enable(False)
         _lib.profile_reset()
-    assert n_norm_fwd == 2 and n_norm_bwd == 0, (n_norm_fwd, n_norm_bwd)
+    # k's norm is one pass; q's runs inside the forward kernel.
+    assert n_norm_fwd == 1 and n_norm_bwd == 0, (n_norm_fwd, n_norm_bwd)
     qh = rnd(O.qk_rms_norm(q))
     kh = rnd(O.qk_rms_norm(k))
     ref = O.sdpa_forward(qh, kh, v, bias=bias, mask=mask, causal=causal, acc_dtype=np.float64)
@@ -161,6 +162,64 @@ def test_fused_qk_norm_backward(name, B, H, s, t, d, dv, kw):
         e = relerr(got.float().cpu().numpy(), want)
         print(f'  {nm} relerr {e:.2e}', flush=True)
         assert e <= tol, (nm, e)
+
+
+@pytest.mark.parametrize('name,d,kw', [
+    ('bf16', 128, {'mask': 'keypad'}),
+    ('f16', 64, {'causal': True}),
+    ('bf16', 256, {}),
+    ('f16', 40, {'bias': True}),
+], ids=['bf16_d128_keypad', 'f16_d64_causal', 'bf16_d256', 'f16_d40_bias'])
+def test_forward_normalises_q_in_the_kernel(name, d, kw):
+    """``nxa_fwd_normed``: the forward normalises its stationary q rows in
+    registers and writes q_hat and the per-row rsqrt for the backward.  q_hat
+    against the oracle's qk_rms_norm rounded to the I/O dtype (one rounding
+    of an fp32 value: at most one ulp from the float64 result), rstd against
+    float64, and the output against the same forward on q normalised by the
+    separate pass (``nxa_rms_norm_fwd``)."""
+    from nitrix_amd import attention as A
+
+    dtype = DT[name]
+    rnd = ROUND[name]
+    rng = np.random.default_rng(zlib.crc32(repr((name, d, sorted(kw))).encode()))
+    B, H, s, t = 2, 3, 300, 170
+    q = rnd(rng.standard_normal((B, H, s, d)).astype(np.float32) * 3)
+    q[0, 0, 5] = rnd(q[0, 0, 5] * 1e-3)  # a row whose mean square is near eps
+    k = rnd(rng.standard_normal((B, H, t, d)).astype(np.float32) * 3)
+    v = rnd(rng.standard_normal((B, H, t, d)).astype(np.float32))
+    to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(_dev(), dtype)  # noqa: E731
+    tq, tk, tv = to(q), to(k), to(v)
+    tb = to(rng.standard_normal((B, H, s, t)).astype(np.float32)) if kw.get('bias') else None
+    tm = None
+    if kw.get('mask') == 'keypad':
+        valid = rng.integers(1, t + 1, size=B)
+        tm = torch.from_numpy((np.arange(t)[None, :] < valid[:, None])[:, None, None, :]).to(_dev())
+    causal = kw.get('causal', False)
+    print(f'[case] nxa_fwd_normed {name} d{d} {kw}', flush=True)
+    kn, _, _ = A._rms_norm_rows(tk)
+    qn = torch.empty_like(tq)
+    rq = torch.empty((B * H * s,), dtype=torch.float32, device=_dev())
+    scale = 1.0 / np.sqrt(d)
+    prep = A._Prepared(tq, kn, tv, tb, tm, scale, causal)
+    o_fused, lse_fused, _ = A._forward(prep, qnorm=(qn, rq))
+    o_nowrite, _, _ = A._forward(prep, qnorm=(None, None))  # a forward without a backward
+    qn2, _, rq2 = A._rms_norm_rows(tq)
+    o_two, lse_two, _ = A._forward(A._Prepared(qn2, kn, tv, tb, tm, scale, causal))
+    torch.cuda.synchronize()
+    want_q = rnd(O.qk_rms_norm(q.astype(np.float64)).astype(np.float32))
+    e_q = relerr(qn.float().cpu().numpy(), want_q)
+    ms = (q.astype(np.float64) ** 2).mean(-1).reshape(-1)
+    e_r = np.abs(rq.cpu().numpy() / (1.0 / np.sqrt(ms + 1e-6)) - 1).max()
+    differ = (qn != qn2).float().mean().item()
+    e_o = relerr(o_fused.float().cpu().numpy(), o_two.float().cpu().numpy())
+    e_l = np.abs(lse_fused.cpu().numpy() - lse_two.cpu().numpy()).max()
+    print(f'  q_hat relerr {e_q:.2e}  rstd relerr {e_r:.2e}  q_hat differing from the '
+          f'separate pass {differ:.2e}  out {e_o:.2e}  lse {e_l:.2e}', flush=True)
+    assert e_q <= TOL[name], e_q
+    assert e_r <= 1e-6, e_r
+    assert differ <= 1e-3, differ  # only fp32 values at a rounding tie can differ
+    assert e_o <= TOL[name] and e_l <= 1e-2, (e_o, e_l)
+    assert torch.equal(o_nowrite, o_fused)
 
 
 def test_qk_norm_outside_the_fused_backward_uses_the_norm_passes():
