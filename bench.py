@@ -141,6 +141,12 @@ CONFIGS = {
         bwd=True,
         workload='bf16 attention fwd+bwd, head dim 256',
     ),
+    'c2f32': dict(
+        io='f32', B=8, H=16, L=4096, D=128, bias=None, mask='keypad', causal=False,
+        bwd=True,
+        workload='fp32 attention fwd+bwd, key-padding mask (C2 in fp32, the dtype of the '
+        "reference's fused kernel)",
+    ),
     'w256f32': dict(
         io='f32', B=1, H=16, L=2048, D=256, bias=None, mask=None, causal=False,
         bwd=True,

@@ -488,7 +488,7 @@ void launch_dkdv(const Params& p, int io_dtype, int dp, hipStream_t stream) {
     launch_dkdv_t<float, 256, kOutDv>(p, stream);
     launch_dkdv_t<float, 256, kOutDk, kColLo>(p, stream);
     launch_dkdv_t<float, 256, kOutDk, kColHi>(p, stream);
-  } else {
+  } else if (!launch_dkdv32(p, dp, stream)) {
     if (dp == 64) launch_dkdv_t<float, 64, kOutBoth>(p, stream);
     else launch_dkdv_t<float, 128, kOutBoth>(p, stream);
   }
@@ -508,7 +508,7 @@ void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream) {
     // fp32 dQ at DP = 256: one pass per half of its columns.
     launch_dq_t<float, 256, kColLo>(p, stream);
     launch_dq_t<float, 256, kColHi>(p, stream);
-  } else {
+  } else if (!launch_dq32(p, dp, stream)) {
     if (dp == 64) launch_dq_t<float, 64>(p, stream);
     else launch_dq_t<float, 128>(p, stream);
   }

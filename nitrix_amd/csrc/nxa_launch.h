@@ -18,6 +18,10 @@ void launch_delta(const Params& p, int io_dtype, hipStream_t stream);
 void launch_dkdv(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dkdv16(const Params& p, int io_dtype, int dp, hipStream_t stream);
+// fp32 dK/dV and dQ at padded head dims 64 / 128 (nxa_bwd32.hip); false when
+// they do not take the problem.
+bool launch_dkdv32(Params p, int dp, hipStream_t stream);
+bool launch_dq32(Params p, int dp, hipStream_t stream);
 void launch_dq16(const Params& p, int io_dtype, int dp, hipStream_t stream);
 // Padded head dim 256 (16-bit I/O), in translation units of their own.
 void launch_fwd16_wide(const Params& p, int io_dtype, hipStream_t stream);
