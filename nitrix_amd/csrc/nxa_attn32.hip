@@ -1,22 +1,24 @@
-// fp32 backward kernels (dK / dV and dQ) at padded head dims 64 and 128.
+// fp32 attention kernels (forward, dK / dV and dQ) at padded head dims 64
+// and 128.
 //
-// Same math as the 16-bit backward and the reference's backward Pallas
-// kernels (src/nitrix/_kernels/cuda/attention.py:272-332 dK/dV, :335-387
-// dQ, :390-499 launches): P = exp2(S scale log2(e) - lse log2(e)) recomputed
-// from the forward's log-sum-exp, dS = P (dP - delta), dV = P^T dO,
-// dK = scale dS^T Q, dQ = scale dS K, fp32 throughout
+// Same math as the 16-bit kernels and the reference's Pallas kernels
+// (src/nitrix/_kernels/cuda/attention.py:85-156 forward, :272-332 dK/dV,
+// :335-387 dQ, :159-264 and :390-499 launches): online base-2 softmax with
+// an fp32 log-sum-exp in the forward; in the backward P = exp2(S scale
+// log2(e) - lse log2(e)) recomputed from it, dS = P (dP - delta),
+// dV = P^T dO, dK = scale dS^T Q, dQ = scale dS K; fp32 throughout
 // (v_mfma_f32_32x32x2_f32).
 //
 // fp32 MFMAs take 64 cycles for 4,096 flops, so these kernels are bound by
 // the matrix core, not by LDS or VALU issue: a block of 4 waves (one per
-// SIMD, up to 512 registers each) holds its 128 keys (dK/dV) or queries (dQ)
-// stationary and streams the other side's [64 x DP] fp32 tiles through a
-// double-buffered LDS ring, filled by direct global -> LDS copies one tile
-// ahead while the current one is consumed.  No transposed copies are made:
-// the products that contract over the streamed rows (dV^T = dO^T P,
-// dK^T = Q^T dS, dQ^T = K^T dS^T) read their A operand as four ds_read_b32
-// per fragment from the row-major tile -- bandwidth the 64-cycle MFMAs leave
-// to spare.  The tiles' 16-byte chunks are XOR-swizzled by row (chunk c of
+// SIMD, up to 512 registers each) holds its 128 queries (forward, dQ) or
+// keys (dK/dV) stationary and streams the other side's [64 x DP] fp32 tiles
+// through a double-buffered LDS ring, filled by direct global -> LDS copies
+// one tile ahead while the current one is consumed.  No transposed copies
+// are made: the products that contract over the streamed rows (O^T = V^T
+// P^T, dV^T = dO^T P, dK^T = Q^T dS, dQ^T = K^T dS^T) read their A operand
+// as four ds_read_b32 per fragment from the row-major tile -- bandwidth the
+// 64-cycle MFMAs leave to spare.  The tiles' 16-byte chunks are XOR-swizzled by row (chunk c of
 // row r at c ^ swz32(r)), which keeps both access patterns free of bank
 // conflicts: 16 consecutive rows of 16-byte reads, and 32 consecutive
 // columns of rows r and r + 4 (r % 8 < 4) of 4-byte reads.
@@ -158,6 +160,237 @@ __device__ __forceinline__ void store_db32(const Params& p, int64_t off, float x
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// Forward.  Block = 4 waves x 32 queries; key tiles of 64 rows.  A wave holds
+// its queries' Q stationary and forms S^T = K Q^T with the query on the
+// lane's column, so the row max and sum take one lane ^ 32 exchange and P^T
+// feeds O^T += V^T P^T from registers.  The running max is raised only when
+// a row's maximum exceeds it by more than kF32Slack (log2 units), so the
+// rescale of O is rare; O and l always accumulate against the same
+// reference, so the result is exact.
+// ---------------------------------------------------------------------------
+constexpr float kF32Slack = 8.0f;
+
+template <int DP, bool HAS_BIAS, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void fwd32_kernel(const Params p) {
+  constexpr int BM = 128, BN = 64, NC = DP / 8, NDB = DP / 32;
+  constexpr int TILE = BN * DP * 4;
+  constexpr int STAGE = 2 * TILE;  // K, V
+  using S = F32Stream<DP>;
+  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+  __shared__ uint32_t lst[kF32MaxTiles];
+
+  const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
+  const int bh = vid / p.nqt;
+  const int qt = p.nqt - 1 - (vid % p.nqt);  // longest (causal) blocks first
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, c32 = lane & 31;
+  const int q0 = qt * BM;
+  const int qw0 = q0 + wave * 32;
+  const int qrow = qw0 + c32;
+  const bool qok = qrow < p.Lq;
+  const int qc = qok ? qrow : p.Lq - 1;
+
+  const float* kp = (const float*)p.k + b * p.k_str[0] + h * p.k_str[1];
+  const float* vp = (const float*)p.v + b * p.v_str[0] + h * p.v_str[1];
+
+  const int k_end = CAUSAL ? min(p.Lk, q0 + BM) : p.Lk;
+  const int nk = (k_end + BN - 1) / BN;
+  const int n = list_tiles(lst, nk, wave, lane, [&](int t) -> int {
+    return p.has_tilemap ? tile_class(p, b, h, q0, q0 + BM, t * BN, t * BN + BN) : 3;
+  });
+
+  f32x4 qf[NC];
+  {
+    const float* qr = (const float*)p.q + b * p.q_str[0] + h * p.q_str[1] + (int64_t)qc * p.q_str[2];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = 8 * c + 4 * g;
+      qf[c] = qok && d < p.D ? *reinterpret_cast<const f32x4*>(qr + d) : f32x4{0, 0, 0, 0};
+    }
+  }
+  const int64_t brow = HAS_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] + (int64_t)qc * p.bias_str[2] : 0;
+  const uint8_t* mrow = p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] + (int64_t)qc * p.mask_str[2] : nullptr;
+
+  f32x16 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
+  float m_ref = -INFINITY, l_i = 0.f;
+
+  S ks, vs_;
+  ks.init(p.k_str[2], p.D, wave, lane);
+  vs_.init(p.v_str[2], p.Dv, wave, lane);
+  F32Offsets<DP> lo;
+  lo.init(g, c32);
+  const uint32_t lds0 = lds_offset(smem);
+  auto issue = [&](int i, int st) NXA_INLINE {
+    const int t = i < n ? (int)(lst[i] & 0xffff) : nk;
+    const uint32_t at = lds0 + st * STAGE;
+    const i32x4 rk = tile_rsrc(kp, p.k_str[2], t * BN, p.Lk, p.D);
+    const i32x4 rv = tile_rsrc(vp, p.v_str[2], t * BN, p.Lk, p.Dv);
+#pragma unroll
+    for (int m = 0; m < S::CNT; ++m) {
+      ks.issue(rk, at, m, wave);
+      vs_.issue(rv, at + TILE, m, wave);
+    }
+  };
+
+  if (n > 0) issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  __syncthreads();
+  for (int i = 0; i < n; ++i) {
+    const int st = i & 1;
+    const uint32_t at = lds0 + st * STAGE;
+    const int t = (int)(lst[i] & 0xffff), cls = (int)(lst[i] >> 16);
+    const int k0 = t * BN;
+    issue(i + 1, st ^ 1);
+
+    // S^T = K Q^T: two 32-key blocks, each over two halves of the head dim
+    // (four independent accumulators), fragments read a step ahead.
+    f32x16 sacc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[u][r] = 0.f;
+    {
+      constexpr int NH = NC / 2;
+      f32x4 a[2][4], bq[4];
+      auto rd = [&](f32x4* x, int c) NXA_INLINE {
+        x[0] = lo.row(at, 0, c);
+        x[1] = lo.row(at, 1, c);
+        x[2] = lo.row(at, 0, c + NH);
+        x[3] = lo.row(at, 1, c + NH);
+      };
+      rd(a[0], 0);
+#pragma unroll
+      for (int c = 0; c < NH; ++c) {
+        if (c + 1 < NH) rd(a[(c + 1) & 1], c + 1);
+        bq[0] = bq[1] = qf[c];
+        bq[2] = bq[3] = qf[c + NH];
+        mma4n<4>(sacc, a[c & 1], bq);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+#pragma unroll
+      for (int c = 0; c + 2 < NH; ++c) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 32, 0);
+    }
+    f32x16 sv[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sv[kb][r] = sacc[kb][r] + sacc[2 + kb][r];
+
+    // Logits.  Fast path (no bias, nothing masked in the tile): the scale
+    // is folded into the exponent's FMA and the max is taken on raw scores.
+    const bool need_mask = p.has_mask && !(cls & 2);
+    const bool tail = k0 + BN > p.Lk;
+    const bool diag = CAUSAL && (k0 + BN - 1 > qw0);
+    const bool general = HAS_BIAS || need_mask || tail || diag || !(p.scale_log2 > 0.f);
+    float cc = p.scale_log2;
+    if (general) {
+      cc = 1.0f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int key0 = k0 + kb * 32 + 8 * c + 4 * g;
+          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (HAS_BIAS) bv = load_bias4(p, p.bias, brow + key0, p.Lk - key0);
+          uint32_t mw = 0x01010101u;
+          if (need_mask) mw = load_mask4(p, mrow + key0, p.Lk - key0);
+          // Every element written exactly once, masked entries a select.
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int key = key0 + e;
+            float x = sv[kb][4 * c + e] * p.scale_log2;
+            if constexpr (HAS_BIAS) x = __builtin_fmaf(bv[e], kLog2e, x);
+            bool keep = mask_bit(mw, e) && key < p.Lk;
+            if (CAUSAL) keep = keep && key <= qrow;
+            sv[kb][4 * c + e] = keep ? x : -INFINITY;
+          }
+        }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sv[kb][r]);
+    mt = fmaxf(mt, shfl_xor32(mt)) * cc;
+    const bool raise = mt > m_ref + kF32Slack;
+    if (__any(raise)) {
+      const float alpha = raise ? fast_exp2(m_ref - mt) : 1.f;
+      m_ref = raise ? mt : m_ref;
+      l_i *= alpha;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+    }
+    const float neg_m = (m_ref == -INFINITY) ? 0.f : -m_ref;
+    float rs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float e = fast_exp2(__builtin_fmaf(sv[kb][r], cc, neg_m));
+        sv[kb][r] = e;
+        rs += e;
+      }
+    l_i += rs;
+
+    // O^T += V^T P^T, the NDB accumulators interleaved, fragments read a
+    // step ahead.
+    {
+      f32x4 a[2][NDB], bb[NDB];
+      auto rd = [&](f32x4* x, int step) NXA_INLINE {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) x[db] = lo.tr(at + TILE, step >> 2, step & 3, db);
+      };
+      rd(a[0], 0);
+#pragma unroll
+      for (int step = 0; step < 8; ++step) {
+        if (step + 1 < 8) rd(a[(step + 1) & 1], step + 1);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) bb[db] = pack4(sv[step >> 2], step & 3);
+        mma4n<NDB>(oacc, a[step & 1], bb);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8 * NDB, 0);
+#pragma unroll
+      for (int step = 0; step < 6; ++step) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4 * NDB, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4 * NDB, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8 * NDB, 0);
+    }
+
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+  }
+
+  // O = O / l (a fully masked row gives 0/0 = NaN, as the reference's
+  // softmax over all -inf logits does), lse = ln sum exp.
+  const float l = l_i + shfl_xor32(l_i);
+  const float inv = 1.0f / l;
+  if (qok) {
+    float* op = (float*)p.o + b * p.o_str[0] + h * p.o_str[1] + (int64_t)qrow * p.o_str[2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d0 = db * 32 + 8 * c + 4 * g;
+        if (d0 < p.Dv) store4(op + d0, oacc[db], 4 * c, inv);
+      }
+    if (g == 0 && p.lse) p.lse[((int64_t)b * p.H + h) * p.Lq + qrow] = (m_ref + __log2f(l)) * kLn2;
+  }
+}
 
 // ---------------------------------------------------------------------------
 // dK / dV (+ dbias).  Block = 4 waves x 32 keys; query tiles of 64 rows.
@@ -607,6 +840,31 @@ __global__ __launch_bounds__(256, 1) void dq32_kernel(const Params p) {
 
 // Launchers: false when the problem is outside what these kernels take
 // (head dim above 128, or more tiles than a block lists).
+bool launch_fwd32(Params p, int dp, hipStream_t stream) {
+  if (dp > 128 || (p.Lk + 63) / 64 > kF32MaxTiles) return false;
+  p.nqt = (p.Lq + 127) / 128;
+  const dim3 grid(p.B * p.H * p.nqt);
+  auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, p); };
+  if (dp == 64) {
+    if (p.has_bias) {
+      if (p.causal) go(fwd32_kernel<64, true, true>);
+      else go(fwd32_kernel<64, true, false>);
+    } else {
+      if (p.causal) go(fwd32_kernel<64, false, true>);
+      else go(fwd32_kernel<64, false, false>);
+    }
+  } else {
+    if (p.has_bias) {
+      if (p.causal) go(fwd32_kernel<128, true, true>);
+      else go(fwd32_kernel<128, true, false>);
+    } else {
+      if (p.causal) go(fwd32_kernel<128, false, true>);
+      else go(fwd32_kernel<128, false, false>);
+    }
+  }
+  return true;
+}
+
 bool launch_dkdv32(Params p, int dp, hipStream_t stream) {
   if (dp > 128 || (p.Lq + 63) / 64 > kF32MaxTiles) return false;
   p.nkt = (p.Lk + 127) / 128;

@@ -534,7 +534,7 @@ static void launch_fwd_flags(const Params& p, hipStream_t stream) {
 void launch_fwd(const Params& p, int io_dtype, int dp, hipStream_t stream) {
   if (io_dtype == kBF16 || io_dtype == kF16) {
     launch_fwd16(p, io_dtype, dp, stream);
-  } else {
+  } else if (!launch_fwd32(p, dp, stream)) {
     if (dp == 64) launch_fwd_flags<float, 64>(p, stream);
     else if (dp == 128) launch_fwd_flags<float, 128>(p, stream);
     else launch_fwd_flags<float, 256>(p, stream);

@@ -18,8 +18,9 @@ void launch_delta(const Params& p, int io_dtype, hipStream_t stream);
 void launch_dkdv(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream);
 void launch_dkdv16(const Params& p, int io_dtype, int dp, hipStream_t stream);
-// fp32 dK/dV and dQ at padded head dims 64 / 128 (nxa_bwd32.hip); false when
+// fp32 forward, dK/dV and dQ at padded head dims 64 / 128 (nxa_attn32.hip); false when
 // they do not take the problem.
+bool launch_fwd32(Params p, int dp, hipStream_t stream);
 bool launch_dkdv32(Params p, int dp, hipStream_t stream);
 bool launch_dq32(Params p, int dp, hipStream_t stream);
 void launch_dq16(const Params& p, int io_dtype, int dp, hipStream_t stream);
