@@ -44,22 +44,22 @@ __device__ __forceinline__ int swz32(int r) {
 // (s % SPR) ^ swz32(row).  Head-dim chunks past D read chunk 0 (finite
 // filler multiplied by the zero padding of the stationary side or never
 // stored); rows past the range's end read zero.
-template <int DP>
+template <int DP, int NW = 4>
 struct F32Stream {
-  static constexpr int SPR = DP / 4;   // 16-byte slots per row
-  static constexpr int CNT = SPR / 4;  // copies per wave per tile
+  static constexpr int SPR = DP / 4;    // 16-byte slots per row
+  static constexpr int CNT = SPR / NW;  // copies per wave per tile (NW waves copy it)
   uint32_t off[CNT];
   __device__ __forceinline__ void init(int64_t rs, int D, int wave, int lane) {
 #pragma unroll
     for (int m = 0; m < CNT; ++m) {
-      const int s = (m * 4 + wave) * 64 + lane;
+      const int s = (m * NW + wave) * 64 + lane;
       const int row = s / SPR;
       const int col = ((s % SPR) ^ swz32(row)) * 4;
       off[m] = 4u * (uint32_t)(row * rs + (col < D ? col : 0));
     }
   }
   __device__ __forceinline__ void issue(i32x4 rsrc, uint32_t lds, int m, int wave) const {
-    dma16_buf(rsrc, off[m], lds + (m * 4 + wave) * 1024);
+    dma16_buf(rsrc, off[m], lds + (m * NW + wave) * 1024);
   }
 };
 
@@ -161,95 +161,20 @@ __device__ __forceinline__ void store_db32(const Params& p, int64_t off, float x
 
 }  // namespace
 
-// ---------------------------------------------------------------------------
-// Forward.  Block = 4 waves x 32 queries; key tiles of 64 rows.  A wave holds
-// its queries' Q stationary and forms S^T = K Q^T with the query on the
-// lane's column, so the row max and sum take one lane ^ 32 exchange and P^T
-// feeds O^T += V^T P^T from registers.  The running max is raised only when
-// a row's maximum exceeds it by more than kF32Slack (log2 units), so the
-// rescale of O is rare; O and l always accumulate against the same
-// reference, so the result is exact.
-// ---------------------------------------------------------------------------
+// Lazy reference raise threshold of the fp32 forward (log2 units).
 constexpr float kF32Slack = 8.0f;
 
+// One 64-key tile of the fp32 forward for a wave's 32 queries: S^T = K Q^T
+// (K rows at `ak`), the online softmax against the wave's running
+// reference, O^T += V^T P^T (V rows at `av`).
 template <int DP, bool HAS_BIAS, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void fwd32_kernel(const Params p) {
-  constexpr int BM = 128, BN = 64, NC = DP / 8, NDB = DP / 32;
-  constexpr int TILE = BN * DP * 4;
-  constexpr int STAGE = 2 * TILE;  // K, V
-  using S = F32Stream<DP>;
-  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
-  __shared__ uint32_t lst[kF32MaxTiles];
-
-  const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
-  const int bh = vid / p.nqt;
-  const int qt = p.nqt - 1 - (vid % p.nqt);  // longest (causal) blocks first
-  const int b = bh / p.H, h = bh % p.H;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 5, c32 = lane & 31;
-  const int q0 = qt * BM;
-  const int qw0 = q0 + wave * 32;
-  const int qrow = qw0 + c32;
-  const bool qok = qrow < p.Lq;
-  const int qc = qok ? qrow : p.Lq - 1;
-
-  const float* kp = (const float*)p.k + b * p.k_str[0] + h * p.k_str[1];
-  const float* vp = (const float*)p.v + b * p.v_str[0] + h * p.v_str[1];
-
-  const int k_end = CAUSAL ? min(p.Lk, q0 + BM) : p.Lk;
-  const int nk = (k_end + BN - 1) / BN;
-  const int n = list_tiles(lst, nk, wave, lane, [&](int t) -> int {
-    return p.has_tilemap ? tile_class(p, b, h, q0, q0 + BM, t * BN, t * BN + BN) : 3;
-  });
-
-  f32x4 qf[NC];
-  {
-    const float* qr = (const float*)p.q + b * p.q_str[0] + h * p.q_str[1] + (int64_t)qc * p.q_str[2];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int d = 8 * c + 4 * g;
-      qf[c] = qok && d < p.D ? *reinterpret_cast<const f32x4*>(qr + d) : f32x4{0, 0, 0, 0};
-    }
-  }
-  const int64_t brow = HAS_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] + (int64_t)qc * p.bias_str[2] : 0;
-  const uint8_t* mrow = p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] + (int64_t)qc * p.mask_str[2] : nullptr;
-
-  f32x16 oacc[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
-  float m_ref = -INFINITY, l_i = 0.f;
-
-  S ks, vs_;
-  ks.init(p.k_str[2], p.D, wave, lane);
-  vs_.init(p.v_str[2], p.Dv, wave, lane);
-  F32Offsets<DP> lo;
-  lo.init(g, c32);
-  const uint32_t lds0 = lds_offset(smem);
-  auto issue = [&](int i, int st) NXA_INLINE {
-    const int t = i < n ? (int)(lst[i] & 0xffff) : nk;
-    const uint32_t at = lds0 + st * STAGE;
-    const i32x4 rk = tile_rsrc(kp, p.k_str[2], t * BN, p.Lk, p.D);
-    const i32x4 rv = tile_rsrc(vp, p.v_str[2], t * BN, p.Lk, p.Dv);
-#pragma unroll
-    for (int m = 0; m < S::CNT; ++m) {
-      ks.issue(rk, at, m, wave);
-      vs_.issue(rv, at + TILE, m, wave);
-    }
-  };
-
-  if (n > 0) issue(0, 0);
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-  __syncthreads();
-  for (int i = 0; i < n; ++i) {
-    const int st = i & 1;
-    const uint32_t at = lds0 + st * STAGE;
-    const int t = (int)(lst[i] & 0xffff), cls = (int)(lst[i] >> 16);
-    const int k0 = t * BN;
-    issue(i + 1, st ^ 1);
-
+__device__ __forceinline__ void fwd32_tile(const Params& p, const F32Offsets<DP>& lo, uint32_t ak,
+                                           uint32_t av, int k0, int cls,
+                                           const f32x4 (&qf)[DP / 8], f32x16 (&oacc)[DP / 32],
+                                           float& m_ref, float& l_i, int64_t brow,
+                                           const uint8_t* mrow, int qrow, int qw0, int g) {
+  constexpr int BN = 64, NC = DP / 8, NDB = DP / 32;
+  const uint32_t at = ak;
     // S^T = K Q^T: two 32-key blocks, each over two halves of the head dim
     // (four independent accumulators), fragments read a step ahead.
     f32x16 sacc[4];
@@ -352,7 +277,7 @@ __global__ __launch_bounds__(256, 1) void fwd32_kernel(const Params p) {
       f32x4 a[2][NDB], bb[NDB];
       auto rd = [&](f32x4* x, int step) NXA_INLINE {
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) x[db] = lo.tr(at + TILE, step >> 2, step & 3, db);
+        for (int db = 0; db < NDB; ++db) x[db] = lo.tr(av, step >> 2, step & 3, db);
       };
       rd(a[0], 0);
 #pragma unroll
@@ -370,6 +295,98 @@ __global__ __launch_bounds__(256, 1) void fwd32_kernel(const Params p) {
       }
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8 * NDB, 0);
     }
+
+}
+
+// ---------------------------------------------------------------------------
+// Forward.  Block = 4 waves x 32 queries; key tiles of 64 rows.  A wave holds
+// its queries' Q stationary and forms S^T = K Q^T with the query on the
+// lane's column, so the row max and sum take one lane ^ 32 exchange and P^T
+// feeds O^T += V^T P^T from registers.  The running max is raised only when
+// a row's maximum exceeds it by more than kF32Slack (log2 units), so the
+// rescale of O is rare; O and l always accumulate against the same
+// reference, so the result is exact.
+// ---------------------------------------------------------------------------
+template <int DP, bool HAS_BIAS, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void fwd32_kernel(const Params p) {
+  constexpr int BM = 128, BN = 64, NC = DP / 8, NDB = DP / 32;
+  constexpr int TILE = BN * DP * 4;
+  constexpr int STAGE = 2 * TILE;  // K, V
+  using S = F32Stream<DP>;
+  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+  __shared__ uint32_t lst[kF32MaxTiles];
+
+  const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
+  const int bh = vid / p.nqt;
+  const int qt = p.nqt - 1 - (vid % p.nqt);  // longest (causal) blocks first
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, c32 = lane & 31;
+  const int q0 = qt * BM;
+  const int qw0 = q0 + wave * 32;
+  const int qrow = qw0 + c32;
+  const bool qok = qrow < p.Lq;
+  const int qc = qok ? qrow : p.Lq - 1;
+
+  const float* kp = (const float*)p.k + b * p.k_str[0] + h * p.k_str[1];
+  const float* vp = (const float*)p.v + b * p.v_str[0] + h * p.v_str[1];
+
+  const int k_end = CAUSAL ? min(p.Lk, q0 + BM) : p.Lk;
+  const int nk = (k_end + BN - 1) / BN;
+  const int n = list_tiles(lst, nk, wave, lane, [&](int t) -> int {
+    return p.has_tilemap ? tile_class(p, b, h, q0, q0 + BM, t * BN, t * BN + BN) : 3;
+  });
+
+  f32x4 qf[NC];
+  {
+    const float* qr = (const float*)p.q + b * p.q_str[0] + h * p.q_str[1] + (int64_t)qc * p.q_str[2];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = 8 * c + 4 * g;
+      qf[c] = qok && d < p.D ? *reinterpret_cast<const f32x4*>(qr + d) : f32x4{0, 0, 0, 0};
+    }
+  }
+  const int64_t brow = HAS_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] + (int64_t)qc * p.bias_str[2] : 0;
+  const uint8_t* mrow = p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] + (int64_t)qc * p.mask_str[2] : nullptr;
+
+  f32x16 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
+  float m_ref = -INFINITY, l_i = 0.f;
+
+  S ks, vs_;
+  ks.init(p.k_str[2], p.D, wave, lane);
+  vs_.init(p.v_str[2], p.Dv, wave, lane);
+  F32Offsets<DP> lo;
+  lo.init(g, c32);
+  const uint32_t lds0 = lds_offset(smem);
+  auto issue = [&](int i, int st) NXA_INLINE {
+    const int t = i < n ? (int)(lst[i] & 0xffff) : nk;
+    const uint32_t at = lds0 + st * STAGE;
+    const i32x4 rk = tile_rsrc(kp, p.k_str[2], t * BN, p.Lk, p.D);
+    const i32x4 rv = tile_rsrc(vp, p.v_str[2], t * BN, p.Lk, p.Dv);
+#pragma unroll
+    for (int m = 0; m < S::CNT; ++m) {
+      ks.issue(rk, at, m, wave);
+      vs_.issue(rv, at + TILE, m, wave);
+    }
+  };
+
+  if (n > 0) issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  __syncthreads();
+  for (int i = 0; i < n; ++i) {
+    const int st = i & 1;
+    const uint32_t at = lds0 + st * STAGE;
+    const int t = (int)(lst[i] & 0xffff), cls = (int)(lst[i] >> 16);
+    const int k0 = t * BN;
+    issue(i + 1, st ^ 1);
+
+    fwd32_tile<DP, HAS_BIAS, CAUSAL>(p, lo, at, at + TILE, k0, cls, qf, oacc, m_ref, l_i, brow,
+                                      mrow, qrow, qw0, g);
 
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
@@ -389,6 +406,134 @@ __global__ __launch_bounds__(256, 1) void fwd32_kernel(const Params p) {
         if (d0 < p.Dv) store4(op + d0, oacc[db], 4 * c, inv);
       }
     if (g == 0 && p.lse) p.lse[((int64_t)b * p.H + h) * p.Lq + qrow] = (m_ref + __log2f(l)) * kLn2;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward of small problems at head dim 64 (few query blocks for 256 CUs):
+// the four waves of a block share 32 queries and split the key tiles
+// between them (wave w takes active tiles w, w + 4, ...), each with K / V
+// stages of its own; at the end the block merges the four partial results
+// in LDS, O = sum_w 2^(m_w - M) O_w and l likewise with M = max_w m_w.
+// Four times the blocks of the 32-query grid, the same arithmetic per tile.
+// ---------------------------------------------------------------------------
+template <bool HAS_BIAS, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void fwd32s_kernel(const Params p) {
+  constexpr int DP = 64, BM = 32, BN = 64, NC = DP / 8, NDB = DP / 32, NW = 4;
+  constexpr int TILE = BN * DP * 4;
+  using S = F32Stream<DP, 1>;
+  __shared__ __attribute__((aligned(16))) char smem[NW * 2 * TILE];
+  __shared__ uint32_t lst[kF32MaxTiles];
+  static_assert(NW * 64 * (NDB * 16 + 2) * 4 <= NW * 2 * TILE, "the merge fits the stages");
+
+  const int vid = xcd_remap(blockIdx.x, p.B * p.H, p.nqt);
+  const int bh = vid / p.nqt;
+  const int qt = p.nqt - 1 - (vid % p.nqt);
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, c32 = lane & 31;
+  const int q0 = qt * BM;
+  const int qrow = q0 + c32;
+  const bool qok = qrow < p.Lq;
+  const int qc = qok ? qrow : p.Lq - 1;
+
+  const float* kp = (const float*)p.k + b * p.k_str[0] + h * p.k_str[1];
+  const float* vp = (const float*)p.v + b * p.v_str[0] + h * p.v_str[1];
+  const int k_end = CAUSAL ? min(p.Lk, q0 + BM) : p.Lk;
+  const int nk = (k_end + BN - 1) / BN;
+  const int n = list_tiles(lst, nk, wave, lane, [&](int t) -> int {
+    return p.has_tilemap ? tile_class(p, b, h, q0, q0 + BM, t * BN, t * BN + BN) : 3;
+  });
+
+  f32x4 qf[NC];
+  {
+    const float* qr = (const float*)p.q + b * p.q_str[0] + h * p.q_str[1] + (int64_t)qc * p.q_str[2];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = 8 * c + 4 * g;
+      qf[c] = qok && d < p.D ? *reinterpret_cast<const f32x4*>(qr + d) : f32x4{0, 0, 0, 0};
+    }
+  }
+  const int64_t brow = HAS_BIAS ? b * p.bias_str[0] + h * p.bias_str[1] + (int64_t)qc * p.bias_str[2] : 0;
+  const uint8_t* mrow = p.has_mask ? p.mask + b * p.mask_str[0] + h * p.mask_str[1] + (int64_t)qc * p.mask_str[2] : nullptr;
+
+  f32x16 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
+  float m_ref = -INFINITY, l_i = 0.f;
+
+  S ks, vs_;
+  ks.init(p.k_str[2], p.D, 0, lane);
+  vs_.init(p.v_str[2], p.Dv, 0, lane);
+  F32Offsets<DP> lo;
+  lo.init(g, c32);
+  const uint32_t at = lds_offset(smem) + wave * 2 * TILE;  // this wave's K, V
+  for (int i = wave; i < n; i += NW) {
+    const int t = (int)(lst[i] & 0xffff), cls = (int)(lst[i] >> 16);
+    const i32x4 rk = tile_rsrc(kp, p.k_str[2], t * BN, p.Lk, p.D);
+    const i32x4 rv = tile_rsrc(vp, p.v_str[2], t * BN, p.Lk, p.Dv);
+#pragma unroll
+    for (int m = 0; m < S::CNT; ++m) {
+      ks.issue(rk, at, m, 0);
+      vs_.issue(rv, at + TILE, m, 0);
+    }
+    // Only this wave reads its stages: its own wait publishes the copies.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    fwd32_tile<DP, HAS_BIAS, CAUSAL>(p, lo, at, at + TILE, t * BN, cls, qf, oacc, m_ref, l_i,
+                                     brow, mrow, qrow, q0, g);
+    // The next copies overwrite the stages the products just read.
+    __builtin_amdgcn_s_waitcnt(lgkmcnt_imm(0));
+  }
+
+  // Merge: [field][wave][lane] floats, fields O (NDB x 16), m, l.
+  __syncthreads();
+  float* ms = reinterpret_cast<float*>(smem);
+  constexpr int F = NDB * 16 + 2;
+  auto slot = [&](int f, int w) -> float& { return ms[(f * NW + w) * 64 + lane]; };
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) slot(db * 16 + r, wave) = oacc[db][r];
+  slot(F - 2, wave) = m_ref;
+  slot(F - 1, wave) = l_i;
+  __syncthreads();
+  if (wave != 0) return;
+  float mw[NW], M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    mw[w] = slot(F - 2, w);
+    M = fmaxf(M, mw[w]);
+  }
+  float sc[NW], l = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    sc[w] = mw[w] == -INFINITY ? 0.f : fast_exp2(mw[w] - M);
+    l = __builtin_fmaf(slot(F - 1, w), sc[w], l);
+  }
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float o = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) o = __builtin_fmaf(slot(db * 16 + r, w), sc[w], o);
+      oacc[db][r] = o;
+    }
+  l += shfl_xor32(l);
+  const float inv = 1.0f / l;
+  if (qok) {
+    float* op = (float*)p.o + b * p.o_str[0] + h * p.o_str[1] + (int64_t)qrow * p.o_str[2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d0 = db * 32 + 8 * c + 4 * g;
+        if (d0 < p.Dv) store4(op + d0, oacc[db], 4 * c, inv);
+      }
+    if (g == 0 && p.lse) p.lse[((int64_t)b * p.H + h) * p.Lq + qrow] = (M + __log2f(l)) * kLn2;
   }
 }
 
@@ -843,6 +988,22 @@ __global__ __launch_bounds__(256, 1) void dq32_kernel(const Params p) {
 bool launch_fwd32(Params p, int dp, hipStream_t stream) {
   if (dp > 128 || (p.Lk + 63) / 64 > kF32MaxTiles) return false;
   p.nqt = (p.Lq + 127) / 128;
+  // Fewer 128-query blocks than a quarter of the CUs, at head dim 64 and
+  // with at least two key tiles: the key-split kernel, four blocks per
+  // 128 queries.
+  if (dp == 64 && p.B * p.H * p.nqt < 64 && p.Lk > 64) {
+    p.nqt = (p.Lq + 31) / 32;
+    const dim3 grid(p.B * p.H * p.nqt);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, p); };
+    if (p.has_bias) {
+      if (p.causal) go(fwd32s_kernel<true, true>);
+      else go(fwd32s_kernel<true, false>);
+    } else {
+      if (p.causal) go(fwd32s_kernel<false, true>);
+      else go(fwd32s_kernel<false, false>);
+    }
+    return true;
+  }
   const dim3 grid(p.B * p.H * p.nqt);
   auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, p); };
   if (dp == 64) {
