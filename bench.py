@@ -184,7 +184,7 @@ def _sparse_blocks(L):
 
 ATTN_SOURCES = ('nxa_common.h', 'nxa_launch.h', 'nxa_fwd16.h', 'nxa_bwd16.h', 'nxa_fwd16.hip',
                 'nxa_fwd16_wide.hip', 'nxa_bwd16.hip', 'nxa_bwd16_wide.hip', 'nxa_fwd.hip',
-                'nxa_bwd.hip', 'nxa_capi.hip', 'nxa_norm.hip')
+                'nxa_bwd.hip', 'nxa_attn32.hip', 'nxa_capi.hip', 'nxa_norm.hip')
 SSM_SOURCES = ('nxa_common.h', 'nxa_ssm.hip')
 
 
