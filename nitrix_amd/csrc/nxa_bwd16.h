@@ -126,6 +126,16 @@ __device__ QTiles build_qtiles(uint16_t* act, uint8_t* acls, uint8_t* cls, int* 
 #ifndef DKDV_PRIO
 #define DKDV_PRIO 1
 #endif
+// dS wave order of the dK/dV kernel: 1 = dS and dK of tile i - 1, then dP of
+// tile i (its VALU phase meets the P wave's S products); 0 = dP, dS, dK of
+// tile i - 1.
+#ifndef DKDV_LAG
+#define DKDV_LAG 1
+#endif
+// Transposed fragments the dK/dV products read ahead of their use.
+#ifndef TRPD
+#define TRPD 4
+#endif
 
 // dbias handling compiled into dK/dV.
 enum : int { kDbNone = 0, kDbFull = 1, kDbColsum = 2 };
@@ -413,17 +423,38 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
       ta[db][0] = vadd(tt, toff[db][0]);
       ta[db][1] = vadd(tt, toff[db][1]);
     }
+    // Product j: query fragment qf = j / NDB (block qf / FPB, fragment
+    // qf % FPB), head-dim block db = j % NDB.  The A fragments (two
+    // transposed reads each) are read TRPD products ahead of their use, so
+    // the reads of later products are in flight while one runs.
+    constexpr int NTR = 2 * FPB * NDB, PT = NTR < TRPD ? NTR : TRPD;
+    auto afrag = [&](int j) NXA_INLINE -> Frag {
+      const int qf = j / NDB, db = j % NDB;
+      const uint32_t ro = (32 * (qf / FPB) + 16 * (qf % FPB)) * (DP * 2);
+      return tr_frag(ta[db][0] + ro, ta[db][1] + ro);
+    };
+    Frag tbuf[PT];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int j = 0; j < PT; ++j) tbuf[j] = afrag(j);
 #pragma unroll
-      for (int f = 0; f < FPB; ++f) {
-        const uint32_t ro = (qb * 32 + 16 * f) * (DP * 2);
+    for (int j = 0; j < NTR; ++j) {
+      const int qf = j / NDB;
+      M::run(acc[j % NDB], tbuf[j % PT], pf[qf / FPB][qf % FPB]);
+      if (j + PT < NTR) tbuf[j % PT] = afrag(j + PT);
+      if constexpr (DBM == kDbColsum)
+        if (!pw && j % NDB == NDB - 1) M::run(csacc, ones, pf[qf / FPB][qf % FPB]);
+    }
+    if constexpr (DBM != kDbColsum) {
+      // Keep that order: PT fragment reads, then one product and one read
+      // at a time.
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
-          M::run(acc[db], tr_frag(ta[db][0] + ro, ta[db][1] + ro), pf[qb][f]);
-        if constexpr (DBM == kDbColsum)
-          if (!pw) M::run(csacc, ones, pf[qb][f]);
+      for (int j = 0; j < PT; ++j) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+#pragma unroll
+      for (int j = 0; j < NTR; ++j) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        if (j + PT < NTR) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
       }
+    }
   };
 
   // P wave, tile t in stage st: P = exp2(S'), published (in fp16) in P buffer
@@ -524,6 +555,45 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
     tr_products(at, pf);
     __builtin_amdgcn_s_setprio(0);
   };
+  // Lagged dS wave, first half: dS and dK^T += Q^T dS of tile t (stage st, P
+  // from buffer `par`) from x = dP - delta, which the previous iteration
+  // formed; the copies of the next tile ride along with the dS pass.
+  auto ds_lag = [&](int t, int st, int par, f32x16 (&x)[2], const TileSrc& s,
+                    int stn) NXA_INLINE {
+    const uint32_t at = lds0 + st * STAGE_BYTES;
+    const int q0 = t * BQ;
+    Frag pf[2][FPB];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+      for (int f = 0; f < FPB; ++f) {
+        const f16x8 pb = *(const lds_pfrag*)(uintptr_t)(poff + par * PB_BYTES + (qb * FPB + f) * 1024);
+        constexpr int CPS = NCPY / (2 * FPB);  // copies per fragment step
+        const int step = qb * FPB + f;
+#pragma unroll
+        for (int j = 0; j < CPS; ++j) copy(s, stn, step * CPS + j);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int r = 8 * f + e;
+          const float ds = __builtin_fmaf((float)pb[e], x[qb][r], 0.0f);
+          x[qb][r] = ds;
+          if constexpr (DBM == kDbFull) {
+            const int q = q0 + qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (kok && q < p.Lq) store_db(p, dbbase + (int64_t)q * p.dbias_str[2], ds);
+          }
+        }
+        pf[qb][f] = M::pack(x[qb], f);
+      }
+    }
+    __builtin_amdgcn_s_setprio(DKDV_PRIO);
+    tr_products(at, pf);
+  };
+  // Lagged dS wave, second half: x = dP - delta of tile t (stage st).
+  auto dp_lag = [&](int st, f32x16 (&x)[2]) NXA_INLINE {
+    f32x16 rows[2];
+    row_products(lds0 + st * STAGE_BYTES, x, rows, [](int) {});
+    __builtin_amdgcn_s_setprio(0);
+  };
 
   // The tile loop is instantiated per role with the same barrier sequence.
   // Iteration i: the P wave handles active tile i, the dS wave tile i - 1
@@ -567,6 +637,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
     int nxt = cur < nq ? tl.tile(1, cur, tclass_g) : nq;
     int k = 0;
     int stc = 0, stp = 2, par = 0;
+    f32x16 xs[2];  // lagged dS wave: dP - delta of the previous tile
     if constexpr (!PW) {
       const TileSrc s0 = tile_src(cur);
 #pragma unroll
@@ -582,6 +653,18 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
         else if (p.qk_norm) stage_krows(stc);
         // P (or the staged rows) is in LDS before the barrier.
         __builtin_amdgcn_s_waitcnt(lgkmcnt_imm(0));
+      } else if constexpr (DKDV_LAG) {
+        const TileSrc s = tile_src(nxt);
+        copy(s, stn, NCPY);
+        if (prv < nq) {
+          ds_lag(prv, stp, par ^ 1, xs, s, stn);
+        } else {
+#pragma unroll
+          for (int j = 0; j < NCPY; ++j) copy(s, stn, j);
+        }
+        if (cur < nq) dp_lag(stc, xs);
+        // Tile nxt is resident before the barrier.
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       } else {
         const TileSrc s = tile_src(nxt);
         copy(s, stn, NCPY);
