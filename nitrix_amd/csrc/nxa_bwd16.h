@@ -470,11 +470,10 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
     const bool tail = q0 + BQ > p.Lq;
     const bool diag = CAUSAL && (kw0 + 31 > q0);
     const bool general = need_mask || tail || diag || bias_rows;
-    Frag pf[2][FPB];
-    // P of query block qb; GEN selects the element-wise pass (per-row mask,
-    // query tail, causal diagonal, per-row bias) and ADD the per-key term,
-    // so interior tiles run straight-line.
-    auto p_block = [&](int qb, auto gen_tag, auto add_tag) NXA_INLINE {
+    // Logits of query block qb in place; GEN selects the element-wise pass
+    // (per-row mask, query tail, causal diagonal, per-row bias) and ADD the
+    // per-key term, so interior tiles run straight-line.
+    auto p_logits = [&](int qb, auto gen_tag, auto add_tag) NXA_INLINE {
       constexpr bool GEN = decltype(gen_tag)::value;
       constexpr bool ADD = decltype(add_tag)::value;
 #pragma unroll
@@ -493,8 +492,13 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
           if (CAUSAL) keep = keep && key <= q;
           xv = keep ? xv : -INFINITY;
         }
-        x[qb][r] = fast_exp2(xv);
+        x[qb][r] = xv;
       }
+    };
+    Frag pf[2][FPB];
+    auto exp_pack = [&](int qb) NXA_INLINE {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[qb][r] = fast_exp2(x[qb][r]);
 #pragma unroll
       for (int f = 0; f < FPB; ++f) {
         pf[qb][f] = M::pack(x[qb], f);
@@ -506,16 +510,31 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
                                         : Mma<f16>::pack(x[qb], f);
       }
     };
-    if (general) {
-      p_block(0, std::true_type{}, std::true_type{});
-      p_block(1, std::true_type{}, std::true_type{});
-    } else if (use_kadd) {
-      p_block(0, std::false_type{}, std::true_type{});
-      p_block(1, std::false_type{}, std::true_type{});
-    } else {
-      p_block(0, std::false_type{}, std::false_type{});
-      p_block(1, std::false_type{}, std::false_type{});
-    }
+    auto p_blocks = [&](auto gen_tag, auto add_tag) NXA_INLINE {
+      if constexpr (DP <= 64) {
+        // All 32 logits before their exponentials: left to itself the
+        // compiler chains FMA -> exp element by element through one
+        // temporary, and at D = 64 that chain's latency, not the issue
+        // rate, sets the pace of the phase (at D = 128 the registers it
+        // would take cost more than the chain).
+        p_logits(0, gen_tag, add_tag);
+        p_logits(1, gen_tag, add_tag);
+        __builtin_amdgcn_sched_barrier(0);
+        exp_pack(0);
+        exp_pack(1);
+      } else {
+        p_logits(0, gen_tag, add_tag);
+        exp_pack(0);
+        p_logits(1, gen_tag, add_tag);
+        exp_pack(1);
+      }
+    };
+    if (general)
+      p_blocks(std::true_type{}, std::true_type{});
+    else if (use_kadd)
+      p_blocks(std::false_type{}, std::true_type{});
+    else
+      p_blocks(std::false_type{}, std::false_type{});
     tr_products(at, pf);
   };
 
