@@ -132,6 +132,11 @@ __device__ QTiles build_qtiles(uint16_t* act, uint8_t* acls, uint8_t* cls, int* 
 #ifndef DKDV_LAG
 #define DKDV_LAG 1
 #endif
+// P wave order of the dK/dV kernel: 1 = dV of tile i - 1, then S and P of
+// tile i; 0 = S, P and dV of tile i.
+#ifndef DKDV_PLAG
+#define DKDV_PLAG 1
+#endif
 // Transposed fragments the dK/dV products read ahead of their use.
 #ifndef TRPD
 #define TRPD 4
@@ -459,7 +464,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
 
   // P wave, tile t in stage st: P = exp2(S'), published (in fp16) in P buffer
   // `par`, then dV^T += dO^T P.
-  auto p_tile = [&](int t, int cls, int st, int par) NXA_INLINE {
+  auto p_tile = [&](int t, int cls, int st, int par, Frag (&pf)[2][FPB]) NXA_INLINE {
     const uint32_t at = lds0 + st * STAGE_BYTES;
     const int q0 = t * BQ;
     __builtin_amdgcn_s_setprio(DKDV_PRIO);  // the exp pass depends on these
@@ -495,7 +500,6 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
         x[qb][r] = xv;
       }
     };
-    Frag pf[2][FPB];
     auto exp_pack = [&](int qb) NXA_INLINE {
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[qb][r] = fast_exp2(x[qb][r]);
@@ -535,7 +539,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
       p_blocks(std::false_type{}, std::true_type{});
     else
       p_blocks(std::false_type{}, std::false_type{});
-    tr_products(at, pf);
+    if constexpr (!DKDV_PLAG) tr_products(at, pf);
   };
 
   // dS wave, tile t in stage st (P from buffer `par`): dP - delta, dS, dK^T
@@ -656,7 +660,8 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
     int nxt = cur < nq ? tl.tile(1, cur, tclass_g) : nq;
     int k = 0;
     int stc = 0, stp = 2, par = 0;
-    f32x16 xs[2];  // lagged dS wave: dP - delta of the previous tile
+    f32x16 xs[2];     // lagged dS wave: dP - delta of the previous tile
+    Frag pfs[2][FPB];  // P wave: P of the current (lagged dV: previous) tile
     if constexpr (!PW) {
       const TileSrc s0 = tile_src(cur);
 #pragma unroll
@@ -668,7 +673,11 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
       const int nn = nxt < nq ? tl.tile(k + 2, nxt, tclass_g) : nq;
       const int stn = stc == 2 ? 0 : stc + 1;
       if constexpr (PW) {
-        if (cur < nq) p_tile(cur, tl.klass(k, cur, tclass_g), stc, par);
+        // Lagged dV: the products of the previous tile open the iteration,
+        // so that the exponentials of this one end it (against the dS
+        // wave's products).
+        if (DKDV_PLAG && prv < nq) tr_products(lds0 + stp * STAGE_BYTES, pfs);
+        if (cur < nq) p_tile(cur, tl.klass(k, cur, tclass_g), stc, par, pfs);
         else if (p.qk_norm) stage_krows(stc);
         // P (or the staged rows) is in LDS before the barrier.
         __builtin_amdgcn_s_waitcnt(lgkmcnt_imm(0));
