@@ -1536,6 +1536,16 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
         M::run(dq[j % NDB], kbuf[j % PQ], pd[j / NDB]);
         if (j + PQ < NQ) kbuf[j % PQ] = kfrag(j + PQ);
       }
+      // Keep that order: PQ fragment reads, then one product and one read
+      // at a time (left to itself the compiler keeps one or two fragments
+      // in flight, and the products wait on their reads).
+#pragma unroll
+      for (int j = 0; j < PQ; ++j) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        if (j + PQ < NQ) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
     }
 
     // Tile i + 1 is resident before the barrier (later tiles may stay in
