@@ -474,57 +474,77 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     auto kfrag = [&](int j) NXA_INLINE -> Frag {
       return *(const lds_frag*)(uintptr_t)(ka[j >> 1] + (j & 1) * (32 * DP * 2));
     };
-    bool fresh = true;  // the first product of each block starts from zero
-    if constexpr (BMODE == kFbTile) {
-      // bias^T fragments: rows = this wave's queries, columns = keys.
-      const uint32_t bt = ldsb + (i % NSTB) * BT_BYTES;
+    // The products of one tile.  LB: the bias products include the 1/scale
+    // remainder l (a wave-uniform choice made once per tile, outside the
+    // straight-line sequence, so that its reads and products schedule as
+    // one block).
+    auto products = [&](auto lb_tag) NXA_INLINE {
+      constexpr bool LB = decltype(lb_tag)::value;
+      // Bias operands, all read before the first product: the bias^T
+      // fragments of the tile (tile mode; rows = this wave's queries,
+      // columns = keys) or the two 32-key row segments (row mode).
+      Frag bfr[2][2];
+      if constexpr (BMODE == kFbTile) {
+        const uint32_t bt = ldsb + (i % NSTB) * BT_BYTES;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const uint32_t b0 = vadd(bt, btoff[kb][0]), b1 = vadd(bt, btoff[kb][1]);
+        for (int kb = 0; kb < 2; ++kb) {
+          const uint32_t b0 = vadd(bt, btoff[kb][0]), b1 = vadd(bt, btoff[kb][1]);
 #pragma unroll
-        for (int f = 0; f < 2; ++f) {
-          const Frag a = tr_frag(b0 + f * (16 * 128), b1 + f * (16 * 128));
-          if (f == 0)
-            S[kb] = M::first(a, bdh[f]);
-          else
-            M::run(S[kb], a, bdh[f]);
-          if (bias_l) M::run(S[kb], a, bdl[f]);
+          for (int f = 0; f < 2; ++f) bfr[kb][f] = tr_frag(b0 + f * (16 * 128), b1 + f * (16 * 128));
+        }
+      } else if constexpr (BMODE == kFbRow) {
+        const T* Bs = ring + (i % NST) * STAGE_ELEMS + 2 * TILE_ELEMS + wave * 128;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          bfr[kb][0] = zero_frag<T>();
+          const T bv = Bs[kb * 32 + c32];
+          bfr[kb][0][0] = g == 0 ? bv : (T)0.f;
         }
       }
-      fresh = false;
-    } else if constexpr (BMODE == kFbRow) {
-      const T* Bs = ring + (i % NST) * STAGE_ELEMS + 2 * TILE_ELEMS + wave * 128;
+      Frag kbuf[PD];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        Frag a = zero_frag<T>();
-        const T bv = Bs[kb * 32 + c32];
-        a[0] = g == 0 ? bv : (T)0.f;
-        S[kb] = M::first(a, bdh[0]);
-        if (bias_l) M::run(S[kb], a, bdl[0]);
+      for (int j = 0; j < PD; ++j) kbuf[j] = kfrag(j);
+      constexpr int NBF = BMODE == kFbTile ? 2 : 1;  // bias fragments per key block
+      if constexpr (MFMA_BIAS) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int f = 0; f < NBF; ++f) {
+            if (f == 0)
+              S[kb] = M::first(bfr[kb][f], bdh[f]);
+            else
+              M::run(S[kb], bfr[kb][f], bdh[f]);
+            if constexpr (LB) M::run(S[kb], bfr[kb][f], bdl[f]);
+          }
       }
-      fresh = false;
-    }
-    Frag kbuf[PD];
 #pragma unroll
-    for (int j = 0; j < PD; ++j) kbuf[j] = kfrag(j);
-#pragma unroll
-    for (int j = 0; j < 2 * NC; ++j) {
-      if (fresh && j < 2)
-        S[j & 1] = M::first(kbuf[j % PD], qf[j >> 1]);
-      else
-        M::run(S[j & 1], kbuf[j % PD], qf[j >> 1]);
-      if (j + PD < 2 * NC) kbuf[j % PD] = kfrag(j + PD);
-    }
-    if constexpr (!MFMA_BIAS) {
-      // Keep that order: PD reads, then one product and one read at a time.
+      for (int j = 0; j < 2 * NC; ++j) {
+        if (!MFMA_BIAS && j < 2)
+          S[j & 1] = M::first(kbuf[j % PD], qf[j >> 1]);
+        else
+          M::run(S[j & 1], kbuf[j % PD], qf[j >> 1]);
+        if (j + PD < 2 * NC) kbuf[j % PD] = kfrag(j + PD);
+      }
+      // Keep that order: the bias reads, PD K reads, the bias products,
+      // then one product and one read at a time.
+      if constexpr (BMODE == kFbTile)
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+      else if constexpr (BMODE == kFbRow)
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
 #pragma unroll
       for (int j = 0; j < PD; ++j) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      if constexpr (MFMA_BIAS)
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * NBF * (LB ? 2 : 1), 0);
 #pragma unroll
       for (int j = 0; j < 2 * NC; ++j) {
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
         if (j + PD < 2 * NC) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
       }
-    }
+    };
+    if (MFMA_BIAS && bias_l)
+      products(std::true_type{});
+    else
+      products(std::false_type{});
   };
 
   // Whether tile i needs the element-wise pass (mask bytes, key tail, causal
