@@ -80,7 +80,7 @@ MEASURED_TRAFFIC = {
 # profiles/selective_scan_valu_counters.md.
 SSM_BWD_VALU_WAVE_INSTS = 2.5654e8
 # Fingerprint of nxa_ssm.hip + nxa_common.h when the counts were taken.
-SSM_VALU_SRC = None  # measured before fingerprints were recorded: stale
+SSM_VALU_SRC = 'fa3803c37f913189'
 SSM_VALU_SOURCE = 'profiles/selective_scan_valu_counters.md (rocprofv3 SQ_INSTS_VALU, SQ_INSTS_VALU_TRANS_F32)'
 PEAK_VALU_TLANEOPS = 256 * 4 * 32 * 2.4e9 / 1e12  # 78.6 T lane-instructions/s
 TRAFFIC_SOURCE = 'profiles/attention_hbm_traffic_c1_c5.md (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1)'
