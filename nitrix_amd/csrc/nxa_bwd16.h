@@ -126,17 +126,6 @@ __device__ QTiles build_qtiles(uint16_t* act, uint8_t* acls, uint8_t* cls, int* 
 #ifndef DKDV_PRIO
 #define DKDV_PRIO 1
 #endif
-// dS wave order of the dK/dV kernel: 1 = dS and dK of tile i - 1, then dP of
-// tile i (its VALU phase meets the P wave's S products); 0 = dP, dS, dK of
-// tile i - 1.
-#ifndef DKDV_LAG
-#define DKDV_LAG 1
-#endif
-// P wave order of the dK/dV kernel: 1 = dV of tile i - 1, then S and P of
-// tile i; 0 = S, P and dV of tile i.
-#ifndef DKDV_PLAG
-#define DKDV_PLAG 1
-#endif
 // Transposed fragments the dK/dV products read ahead of their use.
 #ifndef TRPD
 #define TRPD 4
@@ -163,13 +152,16 @@ __device__ __forceinline__ float load_bias1(const Params& p, int64_t off) {
 //   * the dS wave (w >= 4) holds V stationary and starts at -delta, so its
 //     product is dP - delta; dS = P (dP - delta) with P read back from LDS,
 //     dK^T += Q^T dS (and dbias).
-// S is computed once per tile.  A tile runs in two phases split by a
-// barrier: phase A computes S and P (P wave) and dP (dS wave), phase B dV
-// (P wave) and dS, dK (dS wave); in each phase one wave of a SIMD pair
-// carries the VALU work (exp in A, dS in B) while the other issues MFMAs.
+// S is computed once per tile, and one barrier separates iterations.  In
+// iteration i the P wave runs dV of tile i - 1 (its P kept in registers)
+// and S of tile i, then the exponentials of tile i (publishing P(i)); the
+// dS wave runs dS of tile i - 1 (from the dP - delta it formed in iteration
+// i - 1 and the published P(i - 1)), then dK of tile i - 1 and dP - delta
+// of tile i.  So each wave's VALU phase meets the other's products: the dS
+// pass beside the P wave's dV and S, the exponentials beside dK and dP.
 // Query tiles (Q, dO as swizzled [64 x DP] tiles, -lse2, -delta) move from
-// HBM into a 3-stage LDS ring by direct copies two tiles ahead; each wave
-// waits only for its own copies of the next tile before the tile barrier.
+// HBM into a 3-stage LDS ring by direct copies, which the dS waves issue
+// during their dS pass, one tile ahead.
 //
 // ---------------------------------------------------------------------------
 template <typename T, int DP, bool HAS_BIAS, bool CAUSAL, int DBM>
@@ -539,48 +531,12 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
       p_blocks(std::false_type{}, std::true_type{});
     else
       p_blocks(std::false_type{}, std::false_type{});
-    if constexpr (!DKDV_PLAG) tr_products(at, pf);
   };
 
-  // dS wave, tile t in stage st (P from buffer `par`): dP - delta, dS, dK^T
-  // += Q^T dS (and dbias); the copies of the next tile (sources s, stage
-  // stn) ride along with the row products.
-  auto ds_tile = [&](int t, int st, int par, const TileSrc& s, int stn) NXA_INLINE {
-    const uint32_t at = lds0 + st * STAGE_BYTES;
-    const int q0 = t * BQ;
-    f32x16 x[2], rows[2];
-    row_products(at, x, rows, [&](int j) NXA_INLINE {
-      if (j & 1) copy(s, stn, j >> 1);
-    });
-    __builtin_amdgcn_s_setprio(DKDV_PRIO);  // dS and dK form the longer chain
-    Frag pf[2][FPB];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-#pragma unroll
-      for (int f = 0; f < FPB; ++f) {
-        const f16x8 pb = *(const lds_pfrag*)(uintptr_t)(poff + par * PB_BYTES + (qb * FPB + f) * 1024);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int r = 8 * f + e;
-          // fp16 P times fp32: an FMA with a zero addend on the converted
-          // half, which the compiler emits as one mixed-precision
-          // v_fma_mix_f32 (exact conversion, one rounding).
-          const float ds = __builtin_fmaf((float)pb[e], x[qb][r], 0.0f);
-          x[qb][r] = ds;
-          if constexpr (DBM == kDbFull) {
-            const int q = q0 + qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (kok && q < p.Lq) store_db(p, dbbase + (int64_t)q * p.dbias_str[2], ds);
-          }
-        }
-        pf[qb][f] = M::pack(x[qb], f);
-      }
-    }
-    tr_products(at, pf);
-    __builtin_amdgcn_s_setprio(0);
-  };
-  // Lagged dS wave, first half: dS and dK^T += Q^T dS of tile t (stage st, P
-  // from buffer `par`) from x = dP - delta, which the previous iteration
-  // formed; the copies of the next tile ride along with the dS pass.
+  // dS wave, first half of an iteration: dS and dK^T += Q^T dS (and dbias)
+  // of tile t (stage st, P from buffer `par`) from x = dP - delta, which the
+  // previous iteration formed; the copies of the next tile (sources s,
+  // stage stn) ride along with the dS pass.
   auto ds_lag = [&](int t, int st, int par, f32x16 (&x)[2], const TileSrc& s,
                     int stn) NXA_INLINE {
     const uint32_t at = lds0 + st * STAGE_BYTES;
@@ -611,7 +567,8 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
     __builtin_amdgcn_s_setprio(DKDV_PRIO);
     tr_products(at, pf);
   };
-  // Lagged dS wave, second half: x = dP - delta of tile t (stage st).
+  // dS wave, second half: x = dP - delta of tile t (stage st), for the next
+  // iteration.
   auto dp_lag = [&](int st, f32x16 (&x)[2]) NXA_INLINE {
     f32x16 rows[2];
     row_products(lds0 + st * STAGE_BYTES, x, rows, [](int) {});
@@ -619,11 +576,12 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
   };
 
   // The tile loop is instantiated per role with the same barrier sequence.
-  // Iteration i: the P wave handles active tile i, the dS wave tile i - 1
-  // (whose P the barrier between them published), and the dS waves copy
-  // tile i + 1 into the stage that tile i - 2 left.  Tile i + 2 is looked
-  // up one iteration ahead of its use.
-  // qk-norm: in the last iteration the P waves have no tile; they stage the
+  // Iteration i (active tiles): the P wave forms dV of tile i - 1 and S, P of
+  // tile i; the dS wave dS, dK of tile i - 1 (whose P the barrier between
+  // them published) and dP of tile i; the dS waves copy tile i + 1 into the
+  // stage that tile i - 2 left (no wave reads it in iteration i).  Tile
+  // i + 2 is looked up one iteration ahead of its use.
+  // qk-norm: in the last iteration the P waves have no new tile; they stage the
   // raw rows of their keys (and the rows' rsqrt) into the stage that no one
   // reads then, for the dS waves' norm VJP after the loop, so that no global
   // load waits at the end of the block.  Rows at [wave % 4][key][DP], the
@@ -660,8 +618,8 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
     int nxt = cur < nq ? tl.tile(1, cur, tclass_g) : nq;
     int k = 0;
     int stc = 0, stp = 2, par = 0;
-    f32x16 xs[2];     // lagged dS wave: dP - delta of the previous tile
-    Frag pfs[2][FPB];  // P wave: P of the current (lagged dV: previous) tile
+    f32x16 xs[2];      // dS wave: dP - delta of the tile it forms dS of next
+    Frag pfs[2][FPB];  // P wave: P of the tile whose dV the next iteration forms
     if constexpr (!PW) {
       const TileSrc s0 = tile_src(cur);
 #pragma unroll
@@ -676,12 +634,12 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
         // Lagged dV: the products of the previous tile open the iteration,
         // so that the exponentials of this one end it (against the dS
         // wave's products).
-        if (DKDV_PLAG && prv < nq) tr_products(lds0 + stp * STAGE_BYTES, pfs);
+        if (prv < nq) tr_products(lds0 + stp * STAGE_BYTES, pfs);
         if (cur < nq) p_tile(cur, tl.klass(k, cur, tclass_g), stc, par, pfs);
         else if (p.qk_norm) stage_krows(stc);
         // P (or the staged rows) is in LDS before the barrier.
         __builtin_amdgcn_s_waitcnt(lgkmcnt_imm(0));
-      } else if constexpr (DKDV_LAG) {
+      } else {
         const TileSrc s = tile_src(nxt);
         copy(s, stn, NCPY);
         if (prv < nq) {
@@ -691,17 +649,6 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
           for (int j = 0; j < NCPY; ++j) copy(s, stn, j);
         }
         if (cur < nq) dp_lag(stc, xs);
-        // Tile nxt is resident before the barrier.
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-      } else {
-        const TileSrc s = tile_src(nxt);
-        copy(s, stn, NCPY);
-        if (prv < nq) {
-          ds_tile(prv, stp, par ^ 1, s, stn);
-        } else {
-#pragma unroll
-          for (int j = 0; j < NCPY; ++j) copy(s, stn, j);
-        }
         // Tile nxt is resident before the barrier.
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       }
