@@ -465,7 +465,7 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   // buffer) to cover the LDS latency.
   constexpr int PD = PD_FWD < 2 * NC ? PD_FWD : 2 * NC;
   f32x16 S[2];  // scores of one tile, two 32-key blocks
-  auto qk = [&](int i) NXA_INLINE {
+  auto qk = [&](int i, auto&& between) NXA_INLINE {
     const uint32_t kt = lds0 + (i % NST) * STAGE_BYTES;
     uint32_t ka[NC];
 #pragma unroll
@@ -524,6 +524,7 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
         else
           M::run(S[j & 1], kbuf[j % PD], qf[j >> 1]);
         if (j + PD < 2 * NC) kbuf[j % PD] = kfrag(j + PD);
+        between(j);
       }
       // Keep that order: the bias reads, PD K reads, the bias products,
       // then one product and one read at a time.
@@ -758,7 +759,7 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     // softmax wave of the pair fills the remaining issue slots.
     __builtin_amdgcn_s_setprio(FWD_PRIO);
     if (i > 0) pv(i - 1);
-    if (i < n) qk(i);
+    if (i < n) qk(i, [](int) {});
     __builtin_amdgcn_s_setprio(0);
   };
   // VALU work of tile i: element-wise pass (general tiles), P = exp(...)
@@ -846,8 +847,44 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
         if constexpr (LIST) r = infos_raw(i + 1, i + 1);
         wait_tile(i);
         barrier_nofence();
-        issue_ahead(lt, i, f);
-        qk(i);
+        if constexpr (DP > 128 && BMODE == kFbNone) {
+          // One wave per SIMD: the copies of the next tile ride along with
+          // the S products (one per two), instead of holding the wave at
+          // the copy path before its first product.
+          const bool nx = i + 1 < n;
+          const int k0n = nx ? tile_at(lt, i + 1, f.kv) * BN : 0;
+          const uint32_t atn = lds0 + ((i + 1) % NST) * STAGE_BYTES;
+          const T* kb = kp + (int64_t)k0n * ks;
+          const T* vb = vp + (int64_t)k0n * vs;
+          uint32_t ok[KS::CNT], ov[KS::CNT];
+#pragma unroll
+          for (int m = 0; m < KS::CNT; ++m) {
+            ok[m] = ksm.off[m];
+            ov[m] = vsm.off[m];
+          }
+          if (nx && k0n + BN > p.Lk) {
+            // Tail tile: rows past Lk read the last row.
+#pragma unroll
+            for (int m = 0; m < KS::CNT; ++m) {
+              const int r = min(KS::row_of(m, wave, lane), p.Lk - 1 - k0n);
+              ok[m] = 2u * (uint32_t)(r * ks + KS::col_of(m, wave, lane, p.D));
+              ov[m] = 2u * (uint32_t)(r * vs + KS::col_of(m, wave, lane, p.Dv));
+            }
+          }
+          static_assert(2 * NC == 4 * KS::CNT, "one copy per two S products");
+          qk(i, [&](int j) NXA_INLINE {
+            if (nx && (j & 1)) {
+              const int c = j >> 1;
+              if (c < KS::CNT)
+                dma16_sv(kb, ok[c], atn + (c * NW + wave) * 1024);
+              else
+                dma16_sv(vb, ov[c - KS::CNT], atn + TILE_BYTES + ((c - KS::CNT) * NW + wave) * 1024);
+            }
+          });
+        } else {
+          issue_ahead(lt, i, f);
+          qk(i, [](int) {});
+        }
         valu_phase(lt, i, f.sm);
         pv(i);
         if constexpr (LIST) f = infos_uni(r);
