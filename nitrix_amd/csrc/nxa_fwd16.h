@@ -63,6 +63,11 @@
 #ifndef PD_FWD
 #define PD_FWD 4
 #endif
+// In-step schedule (4-wave blocks): the next tiles' K / V copies ride along
+// with the S products (1) or are issued before them (0).
+#ifndef FWD_COPY_IN_S
+#define FWD_COPY_IN_S 1
+#endif
 
 namespace nxa {
 
@@ -837,6 +842,7 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   } else {
     // In-step: every wave runs S, softmax, O += P V of tile t between
     // barriers t and t+1.
+    constexpr bool COPY_IN_S = FWD_COPY_IN_S && (DP > 128 || BMODE != kFbTile);
     auto run = [&](auto lt) {
       constexpr bool LIST = decltype(lt)::value;
       prologue(lt);
@@ -847,13 +853,19 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
         if constexpr (LIST) r = infos_raw(i + 1, i + 1);
         wait_tile(i);
         barrier_nofence();
-        if constexpr (DP > 128 && BMODE == kFbNone) {
-          // One wave per SIMD: the copies of the next tile ride along with
-          // the S products (one per two), instead of holding the wave at
-          // the copy path before its first product.
-          const bool nx = i + 1 < n;
-          const int k0n = nx ? tile_at(lt, i + 1, f.kv) * BN : 0;
-          const uint32_t atn = lds0 + ((i + 1) % NST) * STAGE_BYTES;
+        if constexpr (COPY_IN_S) {
+          // The K / V copies of tile i + AHEAD ride along with the S
+          // products (one per two), instead of holding the wave at the copy
+          // path before its first product (the row bias copy goes first).
+          const bool nx = i + AHEAD < n;
+          const int k0n = nx ? tile_at(lt, i + AHEAD, f.kv) * BN : 0;
+          const uint32_t atn = lds0 + ((i + AHEAD) % NST) * STAGE_BYTES;
+          if constexpr (BMODE == kFbRow) {
+            if (nx) {
+              const int kk = min(k0n + 2 * c32, p.Lk - 2);
+              dma4_sv(bp, 2u * (uint32_t)kk, atn + 2 * TILE_BYTES + wave * 256);
+            }
+          }
           const T* kb = kp + (int64_t)k0n * ks;
           const T* vb = vp + (int64_t)k0n * vs;
           uint32_t ok[KS::CNT], ov[KS::CNT];
