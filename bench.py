@@ -65,13 +65,13 @@ PEAK_HBM_GBS = 8000.0
 # TRAFFIC_SRC is the fingerprint (_src_fingerprint) of the attention kernel
 # sources the passes ran; when the sources differ, the figure describes other
 # kernels and is reported as stale (traffic null, the old figure beside it).
-TRAFFIC_SRC = 'a61ef6c6d5c71384'
+TRAFFIC_SRC = '6777300c44b6c5ef'
 MEASURED_TRAFFIC = {
     'c1': ('fwd', 6113970),
-    'c2': ('dkdv', 910391300),
-    'c3': ('dkdv', 1619542004),
-    'c4': ('fwd', 4431254876),
-    'c5': ('dkdv', 706497579),
+    'c2': ('dkdv', 910301884),
+    'c3': ('dkdv', 1619900596),
+    'c4': ('fwd', 4431188824),
+    'c5': ('dkdv', 706605480),
 }
 # VALU instructions (wave64) of the selective scan's backward pass (all five
 # kernels) per step at the ssm configuration, transcendental instructions
