@@ -554,6 +554,9 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(const Params p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int r = 8 * f + e;
+          // fp16 P times fp32: an FMA with a zero addend on the converted
+          // half, which the compiler emits as one mixed-precision
+          // v_fma_mix_f32 (exact conversion, one rounding).
           const float ds = __builtin_fmaf((float)pb[e], x[qb][r], 0.0f);
           x[qb][r] = ds;
           if constexpr (DBM == kDbFull) {
