@@ -38,35 +38,44 @@ __device__ __forceinline__ int swz32(int r) {
   return t ^ ((t & 4) << 1);
 }
 
-// [64 x DP] fp32 tiles of one [rows, D] matrix (row stride rs floats), 1 KB
-// direct copies: a tile is DP / 4 copies, CNT per wave of the 4; slot s of
-// the tile holds row s / SPR, physical chunk s % SPR, i.e. logical chunk
-// (s % SPR) ^ swz32(row).  Head-dim chunks past D read chunk 0 (finite
-// filler multiplied by the zero padding of the stationary side or never
-// stored); rows past the range's end read zero.
-template <int DP, int NW = 4>
+// [ROWS x DP] fp32 tiles of one [rows, D] matrix (row stride rs floats),
+// 1 KB direct copies: a tile is ROWS * DP / 256 copies, CNT per wave of the
+// NW; slot s of the tile holds row s / SPR, physical chunk s % SPR, i.e.
+// logical chunk (s % SPR) ^ swz32(row).  Head-dim chunks past D read chunk
+// 0 (finite filler multiplied by the zero padding of the stationary side or
+// never stored); rows past the range's end read zero.  COMPACT keeps one
+// swizzle period (16 rows) of lane offsets and adds the uniform 16-row step
+// at the copy, for kernels short of registers.
+template <int DP, int NW = 4, int ROWS = 64, bool COMPACT = false>
 struct F32Stream {
-  static constexpr int SPR = DP / 4;    // 16-byte slots per row
-  static constexpr int CNT = SPR / NW;  // copies per wave per tile (NW waves copy it)
-  uint32_t off[CNT];
+  static constexpr int SPR = DP / 4;                  // 16-byte slots per row
+  static constexpr int CNT = ROWS * SPR / (64 * NW);  // copies per wave per tile (NW waves copy it)
+  static_assert(ROWS * SPR % (64 * NW) == 0, "tile copies split evenly over the waves");
+  static constexpr int PER = 16 * SPR / (64 * NW);    // copies per 16 rows
+  static constexpr int NOFF = COMPACT && PER >= 1 && CNT % PER == 0 ? PER : CNT;
+  uint32_t off[NOFF];
+  uint32_t step16 = 0;  // bytes of 16 rows
   __device__ __forceinline__ void init(int64_t rs, int D, int wave, int lane) {
 #pragma unroll
-    for (int m = 0; m < CNT; ++m) {
+    for (int m = 0; m < NOFF; ++m) {
       const int s = (m * NW + wave) * 64 + lane;
       const int row = s / SPR;
       const int col = ((s % SPR) ^ swz32(row)) * 4;
       off[m] = 4u * (uint32_t)(row * rs + (col < D ? col : 0));
     }
+    step16 = 64u * (uint32_t)rs;
   }
   __device__ __forceinline__ void issue(i32x4 rsrc, uint32_t lds, int m, int wave) const {
-    dma16_buf(rsrc, off[m], lds + (m * NW + wave) * 1024);
+    const uint32_t o = NOFF == CNT ? off[m] : off[m % NOFF] + (uint32_t)(m / NOFF) * step16;
+    dma16_buf(rsrc, o, lds + (m * NW + wave) * 1024);
   }
 };
 
-// Buffer resource of tile rows r0 .. r0 + 63 of a [n, D] matrix (row stride
-// rs floats): only the rows that exist (an empty range past the end).
+// Buffer resource of tile rows r0 .. r0 + ROWS - 1 of a [n, D] matrix (row
+// stride rs floats): only the rows that exist (an empty range past the end).
+template <int ROWS = 64>
 __device__ __forceinline__ i32x4 tile_rsrc(const float* base, int64_t rs, int r0, int n, int D) {
-  const int rows = min(64, n - r0);
+  const int rows = min(ROWS, n - r0);
   return make_rsrc(base + (int64_t)max(r0, 0) * rs,
                    rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * rs + D) * 4) : 0u);
 }
@@ -96,8 +105,8 @@ __device__ __forceinline__ int list_tiles(uint32_t* lst, int nt, int wave, int l
 //  * Row fragments: lane (g, c32) reads row j*32 + c32, head-dim elements
 //    8c + 4g .. +3, logical chunk 2c + g, physical (2c + g) ^ s with
 //    s = swz32(c32): 2 (c ^ (s >> 1)) + (g ^ (s & 1)).  c ^ (s >> 1) is
-//    (c & 8) + ((c & 7) ^ (s >> 1)), so eight per-lane offsets rowoff[c & 7]
-//    plus an immediate (c & 8) * 32 (+ j * 32 rows) cover every c.
+//    (c & ~7) + ((c & 7) ^ (s >> 1)), so eight per-lane offsets rowoff[c & 7]
+//    plus an immediate (c & ~7) * 32 (+ j * 32 rows) cover every c.
 //  * Transposed fragments: reduction rows q = j*32 + 8f + 4g + i (i = 0..3,
 //    the row groups the accumulator layout gives fragment f), column
 //    d = db*32 + c32: row q, chunk (d / 4) ^ swz32(q), element d % 4.  With
@@ -125,7 +134,7 @@ struct F32Offsets {
   // Row fragment c of 32-row block j.
   __device__ __forceinline__ f32x4 row(uint32_t tile, int j, int c) const {
     typedef __attribute__((address_space(3))) f32x4 lds_f4;
-    return *(const lds_f4*)(uintptr_t)(tile + rowoff[c & 7] + (c & 8) * 32 + j * 32 * ROWB);
+    return *(const lds_f4*)(uintptr_t)(tile + rowoff[c & 7] + (c & ~7) * 32 + j * 32 * ROWB);
   }
   // Transposed fragment: rows j*32 + 8f + 4g + i (i = 0..3), column
   // db*32 + c32.
@@ -798,16 +807,17 @@ __global__ __launch_bounds__(256, 1) void dkdv32_kernel(const Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ.  Block = 4 waves x 32 queries; key tiles of 64 rows.  A wave holds its
+// dQ.  Block = 4 waves x 32 queries; key tiles of 64 rows (32 at head dim
+// 256, so that two stages of K and V fit the LDS).  A wave holds its
 // queries' Q and dO stationary and forms S^T = K Q^T and dP^T = V dO^T with
 // the query on the lane's column, so dS^T feeds dQ^T += K^T dS^T.
 // ---------------------------------------------------------------------------
 template <int DP, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void dq32_kernel(const Params p) {
-  constexpr int BM = 128, BN = 64, NC = DP / 8, NDB = DP / 32;
+  constexpr int BM = 128, BN = DP > 128 ? 32 : 64, NKB = BN / 32, NC = DP / 8, NDB = DP / 32;
   constexpr int TILE = BN * DP * 4;
   constexpr int STAGE = 2 * TILE;  // K, V
-  using S = F32Stream<DP>;
+  using S = F32Stream<DP, 4, BN, (DP > 128)>;
   __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
   __shared__ uint32_t lst[kF32MaxTiles];
 
@@ -862,8 +872,8 @@ __global__ __launch_bounds__(256, 1) void dq32_kernel(const Params p) {
   auto issue = [&](int i, int st) NXA_INLINE {
     const int t = i < n ? (int)(lst[i] & 0xffff) : nk;
     const uint32_t at = lds0 + st * STAGE;
-    const i32x4 rk = tile_rsrc(kp, p.k_str[2], t * BN, p.Lk, p.D);
-    const i32x4 rv = tile_rsrc(vp, p.v_str[2], t * BN, p.Lk, p.Dv);
+    const i32x4 rk = tile_rsrc<BN>(kp, p.k_str[2], t * BN, p.Lk, p.D);
+    const i32x4 rv = tile_rsrc<BN>(vp, p.v_str[2], t * BN, p.Lk, p.Dv);
 #pragma unroll
     for (int m = 0; m < S::CNT; ++m) {
       ks.issue(rk, at, m, wave);
@@ -884,43 +894,48 @@ __global__ __launch_bounds__(256, 1) void dq32_kernel(const Params p) {
     const int k0 = t * BN;
     issue(i + 1, st ^ 1);
 
-    f32x16 acc[4];  // S^T of key blocks 0, 1, then dP^T
+    constexpr int NA = 2 * NKB;  // S^T of each 32-key block, then dP^T
+    f32x16 acc[NA];
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
+    for (int n = 0; n < NA; ++n)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
     {
-      f32x4 a[2][4], bq[4];
+      f32x4 a[2][NA], bq[NA];
       auto rd = [&](f32x4* x, int c) NXA_INLINE {
-        x[0] = lo.row(at, 0, c);
-        x[1] = lo.row(at, 1, c);
-        x[2] = lo.row(at + TILE, 0, c);
-        x[3] = lo.row(at + TILE, 1, c);
+#pragma unroll
+        for (int j = 0; j < NKB; ++j) {
+          x[j] = lo.row(at, j, c);
+          x[NKB + j] = lo.row(at + TILE, j, c);
+        }
       };
       rd(a[0], 0);
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         if (c + 1 < NC) rd(a[(c + 1) & 1], c + 1);
-        bq[0] = bq[1] = qf[c];
-        bq[2] = bq[3] = df[c];
-        mma4n<4>(acc, a[c & 1], bq);
+#pragma unroll
+        for (int j = 0; j < NKB; ++j) {
+          bq[j] = qf[c];
+          bq[NKB + j] = df[c];
+        }
+        mma4n<NA>(acc, a[c & 1], bq);
       }
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * NA, 0);
 #pragma unroll
       for (int c = 0; c + 2 < NC; ++c) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 16, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4 * NA, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, NA, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 32, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8 * NA, 0);
     }
     f32x16* s = acc;
-    f32x16* dp = acc + 2;
+    f32x16* dp = acc + NKB;
 
     const bool need_mask = p.has_mask && !(cls & 2);
     const bool diag = CAUSAL && (k0 + BN - 1 > qw0);
     const bool tail = k0 + BN > p.Lk;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NKB; ++j)
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int key0 = k0 + j * 32 + 8 * c + 4 * g;
@@ -942,29 +957,34 @@ __global__ __launch_bounds__(256, 1) void dq32_kernel(const Params p) {
         }
       }
 
-    // dQ^T += K^T dS^T, the NDB accumulators interleaved, fragments read a
+    // dQ^T += K^T dS^T, the accumulators of a group of NDH column blocks
+    // interleaved (all NDB at once, or, at head dim 256, one half and then
+    // the other, which halves the read-ahead registers), fragments read a
     // step ahead.
     {
-      f32x4 a[2][NDB], bb[NDB];
-      auto rd = [&](f32x4* x, int step) NXA_INLINE {
+      constexpr int NH = NDB > 4 ? 2 : 1, NDH = NDB / NH, NS = 4 * NKB, NU = NH * NS;
+      f32x4 a[2][NDH], bb[NDH];
+      auto rd = [&](f32x4* x, int u) NXA_INLINE {
+        const int step = u % NS, d0 = (u / NS) * NDH;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) x[db] = lo.tr(at, step >> 2, step & 3, db);
+        for (int k = 0; k < NDH; ++k) x[k] = lo.tr(at, step >> 2, step & 3, d0 + k);
       };
       rd(a[0], 0);
 #pragma unroll
-      for (int step = 0; step < 8; ++step) {
-        if (step + 1 < 8) rd(a[(step + 1) & 1], step + 1);
+      for (int u = 0; u < NU; ++u) {
+        if (u + 1 < NU) rd(a[(u + 1) & 1], u + 1);
+        const int step = u % NS;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) bb[db] = pack4(dp[step >> 2], step & 3);
-        mma4n<NDB>(dq, a[step & 1], bb);
+        for (int k = 0; k < NDH; ++k) bb[k] = pack4(dp[step >> 2], step & 3);
+        mma4n<NDH>(dq + (u / NS) * NDH, a[u & 1], bb);
       }
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8 * NDB, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8 * NDH, 0);
 #pragma unroll
-      for (int step = 0; step < 6; ++step) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4 * NDB, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4 * NDB, 0);
+      for (int u = 0; u + 2 < NU; ++u) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4 * NDH, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4 * NDH, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8 * NDB, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8 * NDH, 0);
     }
 
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -1041,12 +1061,16 @@ bool launch_dkdv32(Params p, int dp, hipStream_t stream) {
 }
 
 bool launch_dq32(Params p, int dp, hipStream_t stream) {
-  if (dp > 128 || (p.Lk + 63) / 64 > kF32MaxTiles) return false;
+  const int bn = dp > 128 ? 32 : 64;
+  if (dp > 256 || (p.Lk + bn - 1) / bn > kF32MaxTiles) return false;
   p.nqt = (p.Lq + 127) / 128;
   const dim3 grid(p.B * p.H * p.nqt);
   if (dp == 64) {
     if (p.causal) hipLaunchKernelGGL((dq32_kernel<64, true>), grid, dim3(256), 0, stream, p);
     else hipLaunchKernelGGL((dq32_kernel<64, false>), grid, dim3(256), 0, stream, p);
+  } else if (dp == 256) {
+    if (p.causal) hipLaunchKernelGGL((dq32_kernel<256, true>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((dq32_kernel<256, false>), grid, dim3(256), 0, stream, p);
   } else {
     if (p.causal) hipLaunchKernelGGL((dq32_kernel<128, true>), grid, dim3(256), 0, stream, p);
     else hipLaunchKernelGGL((dq32_kernel<128, false>), grid, dim3(256), 0, stream, p);

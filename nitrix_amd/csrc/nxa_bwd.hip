@@ -504,13 +504,16 @@ static void launch_dq_t(Params p, hipStream_t stream) {
 void launch_dq(const Params& p, int io_dtype, int dp, hipStream_t stream) {
   if (io_dtype == kBF16 || io_dtype == kF16) {
     launch_dq16(p, io_dtype, dp, stream);
-  } else if (dp == 256) {
-    // fp32 dQ at DP = 256: one pass per half of its columns.
-    launch_dq_t<float, 256, kColLo>(p, stream);
-    launch_dq_t<float, 256, kColHi>(p, stream);
   } else if (!launch_dq32(p, dp, stream)) {
-    if (dp == 64) launch_dq_t<float, 64>(p, stream);
-    else launch_dq_t<float, 128>(p, stream);
+    if (dp == 256) {
+      // fp32 dQ at DP = 256: one pass per half of its columns.
+      launch_dq_t<float, 256, kColLo>(p, stream);
+      launch_dq_t<float, 256, kColHi>(p, stream);
+    } else if (dp == 64) {
+      launch_dq_t<float, 64>(p, stream);
+    } else {
+      launch_dq_t<float, 128>(p, stream);
+    }
   }
 }
 
