@@ -546,18 +546,27 @@ __global__ __launch_bounds__(256, 1) void fwd32s_kernel(const Params p) {
   }
 }
 
+// Outputs of one dK / dV launch.
+enum : int { kF32Dv = 1, kF32Dk = 2, kF32Both = 3 };
+
 // ---------------------------------------------------------------------------
 // dK / dV (+ dbias).  Block = 4 waves x 32 keys; query tiles of 64 rows.
 // A wave holds its keys' K and V stationary and forms S = Q K^T and
 // dP = dO V^T with the key on the lane's column, so P and dS feed
-// dV^T += dO^T P and dK^T += Q^T dS from registers.
+// dV^T += dO^T P and dK^T += Q^T dS from registers.  At head dim 256 the
+// stationary rows and both accumulator sets do not fit one wave's
+// registers: two launches, OUT = kF32Dv (K stationary; S, P, dV) and then
+// kF32Dk (K, V stationary; S, dP, dS, dK, dbias), over 32-query tiles.
 // ---------------------------------------------------------------------------
-template <int DP, bool CAUSAL>
+template <int DP, bool CAUSAL, int OUT = kF32Both>
 __global__ __launch_bounds__(256, 1) void dkdv32_kernel(const Params p) {
-  constexpr int BNK = 128, BQ = 64, NC = DP / 8, NDB = DP / 32;
+  constexpr bool DV = OUT & kF32Dv, DK = OUT & kF32Dk;
+  static_assert(OUT == kF32Both || DP > 128, "split launches are for head dim 256");
+  constexpr int BNK = 128, BQ = OUT == kF32Both ? 64 : 32, NQB = BQ / 32;
+  constexpr int NC = DP / 8, NDB = DP / 32;
   constexpr int TILE = BQ * DP * 4;
   constexpr int STAGE = 2 * TILE + 2 * BQ * 4;  // Q, dO, -lse log2(e), -delta
-  using S = F32Stream<DP>;
+  using S = F32Stream<DP, 4, BQ, (DP > 128)>;
   __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
   __shared__ uint32_t lst[kF32MaxTiles];
 
@@ -586,7 +595,8 @@ __global__ __launch_bounds__(256, 1) void dkdv32_kernel(const Params p) {
     return p.has_tilemap ? tile_class(p, b, h, q0, q0 + BQ, kblk0, kblk0 + BNK) : 3;
   });
 
-  // Stationary K and V rows of the lane's key (B operands).
+  // Stationary K and V rows of the lane's key (B operands; V only where dP
+  // is formed).
   f32x4 kf[NC], vf[NC];
   {
     const float* kr = (const float*)p.k + b * p.k_str[0] + h * p.k_str[1] + (int64_t)kc * p.k_str[2];
@@ -595,7 +605,8 @@ __global__ __launch_bounds__(256, 1) void dkdv32_kernel(const Params p) {
     for (int c = 0; c < NC; ++c) {
       const int d = 8 * c + 4 * g;
       kf[c] = kok && d < p.D ? *reinterpret_cast<const f32x4*>(kr + d) : f32x4{0, 0, 0, 0};
-      vf[c] = kok && d < p.Dv ? *reinterpret_cast<const f32x4*>(vr + d) : f32x4{0, 0, 0, 0};
+      if constexpr (DK)
+        vf[c] = kok && d < p.Dv ? *reinterpret_cast<const f32x4*>(vr + d) : f32x4{0, 0, 0, 0};
     }
   }
   f32x16 dk[NDB], dv[NDB];
@@ -613,25 +624,26 @@ __global__ __launch_bounds__(256, 1) void dkdv32_kernel(const Params p) {
   const uint32_t lds0 = lds_offset(smem);
 
   // Copies of active tile i (empty ranges past the list) into stage st:
-  // CNT Q and CNT dO copies, and 16 rows of -lse log2(e) and -delta per
-  // wave (lanes 0-15).
+  // CNT Q and CNT dO copies, and BQ / 4 rows of -lse log2(e) and -delta per
+  // wave (lanes 0 .. BQ / 4 - 1).
   auto issue = [&](int i, int st) NXA_INLINE {
     const int t = i < n ? (int)(lst[i] & 0xffff) : nq;
     const int q0 = t * BQ;
     const uint32_t at = lds0 + st * STAGE;
-    const i32x4 rq = tile_rsrc(qp, p.q_str[2], q0, p.Lq, p.D);
-    const i32x4 ro = tile_rsrc(dop, p.o_str[2], q0, p.Lq, p.Dv);
+    const i32x4 rq = tile_rsrc<BQ>(qp, p.q_str[2], q0, p.Lq, p.D);
+    const i32x4 ro = tile_rsrc<BQ>(dop, p.o_str[2], q0, p.Lq, p.Dv);
 #pragma unroll
     for (int m = 0; m < S::CNT; ++m) {
       qs.issue(rq, at, m, wave);
       ds_.issue(ro, at + TILE, m, wave);
     }
     const int rows = max(min(BQ, p.Lq - q0), 0);
-    if (lane < 16) {
-      dma4_buf(make_rsrc(nlp + min(q0, p.Lq), (uint32_t)rows * 4u), 4u * (16 * wave + lane),
-               at + 2 * TILE + 64 * wave);
-      dma4_buf(make_rsrc(ndp + min(q0, p.Lq), (uint32_t)rows * 4u), 4u * (16 * wave + lane),
-               at + 2 * TILE + BQ * 4 + 64 * wave);
+    constexpr int RW = BQ / 4;  // row values per wave
+    if (lane < RW) {
+      dma4_buf(make_rsrc(nlp + min(q0, p.Lq), (uint32_t)rows * 4u), 4u * (RW * wave + lane),
+               at + 2 * TILE + 4 * RW * wave);
+      dma4_buf(make_rsrc(ndp + min(q0, p.Lq), (uint32_t)rows * 4u), 4u * (RW * wave + lane),
+               at + 2 * TILE + BQ * 4 + 4 * RW * wave);
     }
   };
   constexpr int CPT = 2 * S::CNT + 2;  // copies per wave per tile
@@ -642,7 +654,7 @@ __global__ __launch_bounds__(256, 1) void dkdv32_kernel(const Params p) {
   const bool full_db = p.dbias_mode == kDbiasFull;
 
   if (n > 0) issue(0, 0);
-  if (full_db && kok) {
+  if (DK && full_db && kok) {
     // A full dbias gets zeros where no query of a tile keeps this key block.
     int li = 0;
     for (int t = 0; t < nq; ++t) {
@@ -663,41 +675,65 @@ __global__ __launch_bounds__(256, 1) void dkdv32_kernel(const Params p) {
     const int q0 = t * BQ;
     issue(i + 1, st ^ 1);
 
-    // S = Q K^T and dP = dO V^T, two 32-query blocks.
-    // acc[0..1] = S of query blocks 0, 1; acc[2..3] = dP.  The A fragments
-    // of step c + 1 are read while the MFMAs of step c run.
-    f32x16 acc[4];
+    // S = Q K^T and dP = dO V^T.  Both outputs: acc[0..1] = S of query
+    // blocks 0, 1, acc[2..3] = dP.  dK: acc[0] = S, acc[1] = dP of the one
+    // 32-query block.  dV: S over the low and the high half of the head
+    // dim, summed after.  The A fragments of step c + 1 are read while the
+    // MFMAs of step c run.
+    constexpr int NA = OUT == kF32Both ? 4 : 2;
+    constexpr int NSTEP = OUT == kF32Dv ? NC / 2 : NC;
+    f32x16 acc[NA];
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
+    for (int n = 0; n < NA; ++n)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
     {
-      f32x4 a[2][4], bq[4];
+      f32x4 a[2][NA], bq[NA];
       auto rd = [&](f32x4* x, int c) NXA_INLINE {
-        x[0] = lo.row(at, 0, c);
-        x[1] = lo.row(at, 1, c);
-        x[2] = lo.row(at + TILE, 0, c);
-        x[3] = lo.row(at + TILE, 1, c);
+        if constexpr (OUT == kF32Both) {
+          x[0] = lo.row(at, 0, c);
+          x[1] = lo.row(at, 1, c);
+          x[2] = lo.row(at + TILE, 0, c);
+          x[3] = lo.row(at + TILE, 1, c);
+        } else if constexpr (OUT == kF32Dk) {
+          x[0] = lo.row(at, 0, c);
+          x[1] = lo.row(at + TILE, 0, c);
+        } else {
+          x[0] = lo.row(at, 0, c);
+          x[1] = lo.row(at, 0, c + NC / 2);
+        }
       };
       rd(a[0], 0);
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        if (c + 1 < NC) rd(a[(c + 1) & 1], c + 1);
-        bq[0] = bq[1] = kf[c];
-        bq[2] = bq[3] = vf[c];
-        mma4n<4>(acc, a[c & 1], bq);
+      for (int c = 0; c < NSTEP; ++c) {
+        if (c + 1 < NSTEP) rd(a[(c + 1) & 1], c + 1);
+        if constexpr (OUT == kF32Both) {
+          bq[0] = bq[1] = kf[c];
+          bq[2] = bq[3] = vf[c];
+        } else if constexpr (OUT == kF32Dk) {
+          bq[0] = kf[c];
+          bq[1] = vf[c];
+        } else {
+          bq[0] = kf[c];
+          bq[1] = kf[c + NC / 2];
+        }
+        mma4n<NA>(acc, a[c & 1], bq);
       }
       // The next step's fragments ahead of this step's products.
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * NA, 0);
 #pragma unroll
-      for (int c = 0; c + 2 < NC; ++c) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 16, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+      for (int c = 0; c + 2 < NSTEP; ++c) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4 * NA, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, NA, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 32, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8 * NA, 0);
+    }
+    if constexpr (OUT == kF32Dv) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[0][r] += acc[1][r];
     }
     f32x16* s = acc;
-    f32x16* dp = acc + 2;
+    f32x16* dp = acc + NQB;
 
     // P and dS, element by element (the query is the accumulator row).
     typedef __attribute__((address_space(3))) f32x4 lds_f4;
@@ -705,7 +741,7 @@ __global__ __launch_bounds__(256, 1) void dkdv32_kernel(const Params p) {
     const bool diag = CAUSAL && (kw0 + 31 > q0);
     const bool tail = (q0 + BQ > p.Lq) || (kw0 + 32 > p.Lk);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NQB; ++j)
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int ql0 = j * 32 + 8 * c + 4 * g;
@@ -725,20 +761,51 @@ __global__ __launch_bounds__(256, 1) void dkdv32_kernel(const Params p) {
           if (tail) keep = keep && q < p.Lq && kok;
           if (diag) keep = keep && key <= q;
           const float pr = keep ? fast_exp2(x) : 0.f;
-          const float dsv = pr * (dp[j][r] + nd[e]);
-          s[j][r] = pr;
-          dp[j][r] = dsv;
-          if (full_db && kok && q < p.Lq) store_db32(p, dbbase + (int64_t)q * p.dbias_str[2], dsv);
-          colsum += dsv;
+          if constexpr (DV) s[j][r] = pr;
+          if constexpr (DK) {
+            const float dsv = pr * (dp[j][r] + nd[e]);
+            dp[j][r] = dsv;
+            if (full_db && kok && q < p.Lq) store_db32(p, dbbase + (int64_t)q * p.dbias_str[2], dsv);
+            colsum += dsv;
+          }
         }
       }
 
     // dV^T += dO^T P and dK^T += Q^T dS (A operands read transposed), in
     // halves of the head dim: four accumulators (dV and dK of two 32-column
     // blocks) interleaved, the fragments of the next step read during this
-    // one.
+    // one.  A launch with one output: groups of four of its column blocks,
+    // read ahead across the groups.
+    if constexpr (OUT != kF32Both) {
+      constexpr int NDH = 4, NS = 4 * NQB, NU = (NDB / NDH) * NS;
+      f32x16* o = DV ? dv : dk;
+      f32x16* pb = DV ? s : dp;
+      const uint32_t src = DV ? at + TILE : at;  // dO or Q
+      f32x4 a[2][NDH], bb[NDH];
+      auto rd = [&](f32x4* x, int u) NXA_INLINE {
+        const int step = u % NS, d0 = (u / NS) * NDH;
 #pragma unroll
-    for (int hb = 0; hb < NDB; hb += 2) {
+        for (int k = 0; k < NDH; ++k) x[k] = lo.tr(src, step >> 2, step & 3, d0 + k);
+      };
+      rd(a[0], 0);
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        if (u + 1 < NU) rd(a[(u + 1) & 1], u + 1);
+        const int step = u % NS;
+#pragma unroll
+        for (int k = 0; k < NDH; ++k) bb[k] = pack4(pb[step >> 2], step & 3);
+        mma4n<NDH>(o + (u / NS) * NDH, a[u & 1], bb);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8 * NDH, 0);
+#pragma unroll
+      for (int u = 0; u + 2 < NU; ++u) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4 * NDH, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4 * NDH, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8 * NDH, 0);
+    }
+#pragma unroll
+    for (int hb = 0; hb < (OUT == kF32Both ? NDB : 0); hb += 2) {
       constexpr int NA = NDB >= 2 ? 4 : 2;
       f32x16 o[NA];
 #pragma unroll
@@ -796,11 +863,11 @@ __global__ __launch_bounds__(256, 1) void dkdv32_kernel(const Params p) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int d0 = db * 32 + 8 * c + 4 * g;
-        if (d0 < p.D) store4(dkp + d0, dk[db], 4 * c, p.scale);
-        if (d0 < p.Dv) store4(dvp + d0, dv[db], 4 * c, 1.0f);
+        if (DK && d0 < p.D) store4(dkp + d0, dk[db], 4 * c, p.scale);
+        if (DV && d0 < p.Dv) store4(dvp + d0, dv[db], 4 * c, 1.0f);
       }
   }
-  if (p.dbias_mode == kDbiasColsum) {
+  if (DK && p.dbias_mode == kDbiasColsum) {
     const float tot = colsum + shfl_xor32(colsum);
     if (kok && g == 0) store_db32(p, dbbase, tot);
   }
@@ -1047,10 +1114,20 @@ bool launch_fwd32(Params p, int dp, hipStream_t stream) {
 }
 
 bool launch_dkdv32(Params p, int dp, hipStream_t stream) {
-  if (dp > 128 || (p.Lq + 63) / 64 > kF32MaxTiles) return false;
+  const int bq = dp > 128 ? 32 : 64;
+  if (dp > 256 || (p.Lq + bq - 1) / bq > kF32MaxTiles) return false;
   p.nkt = (p.Lk + 127) / 128;
   const dim3 grid(p.nbh * p.nkt);
-  if (dp == 64) {
+  if (dp == 256) {
+    // dV, then dK and dbias.
+    if (p.causal) {
+      hipLaunchKernelGGL((dkdv32_kernel<256, true, kF32Dv>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((dkdv32_kernel<256, true, kF32Dk>), grid, dim3(256), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((dkdv32_kernel<256, false, kF32Dv>), grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((dkdv32_kernel<256, false, kF32Dk>), grid, dim3(256), 0, stream, p);
+    }
+  } else if (dp == 64) {
     if (p.causal) hipLaunchKernelGGL((dkdv32_kernel<64, true>), grid, dim3(256), 0, stream, p);
     else hipLaunchKernelGGL((dkdv32_kernel<64, false>), grid, dim3(256), 0, stream, p);
   } else {

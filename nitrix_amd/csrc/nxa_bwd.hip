@@ -483,14 +483,17 @@ static void launch_dkdv_t(Params p, hipStream_t stream) {
 void launch_dkdv(const Params& p, int io_dtype, int dp, hipStream_t stream) {
   if (io_dtype == kBF16 || io_dtype == kF16) {
     launch_dkdv16(p, io_dtype, dp, stream);
-  } else if (dp == 256) {
-    // fp32 at DP = 256: dV, then dK in two column halves.
-    launch_dkdv_t<float, 256, kOutDv>(p, stream);
-    launch_dkdv_t<float, 256, kOutDk, kColLo>(p, stream);
-    launch_dkdv_t<float, 256, kOutDk, kColHi>(p, stream);
   } else if (!launch_dkdv32(p, dp, stream)) {
-    if (dp == 64) launch_dkdv_t<float, 64, kOutBoth>(p, stream);
-    else launch_dkdv_t<float, 128, kOutBoth>(p, stream);
+    if (dp == 256) {
+      // fp32 at DP = 256: dV, then dK in two column halves.
+      launch_dkdv_t<float, 256, kOutDv>(p, stream);
+      launch_dkdv_t<float, 256, kOutDk, kColLo>(p, stream);
+      launch_dkdv_t<float, 256, kOutDk, kColHi>(p, stream);
+    } else if (dp == 64) {
+      launch_dkdv_t<float, 64, kOutBoth>(p, stream);
+    } else {
+      launch_dkdv_t<float, 128, kOutBoth>(p, stream);
+    }
   }
 }
 
