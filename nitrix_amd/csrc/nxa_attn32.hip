@@ -173,54 +173,57 @@ __device__ __forceinline__ void store_db32(const Params& p, int64_t off, float x
 // Lazy reference raise threshold of the fp32 forward (log2 units).
 constexpr float kF32Slack = 8.0f;
 
-// One 64-key tile of the fp32 forward for a wave's 32 queries: S^T = K Q^T
-// (K rows at `ak`), the online softmax against the wave's running
-// reference, O^T += V^T P^T (V rows at `av`).
-template <int DP, bool HAS_BIAS, bool CAUSAL>
+// One key tile (BN = 64, or 32 at head dim 256) of the fp32 forward for a
+// wave's 32 queries: S^T = K Q^T (K rows at `ak`), the online softmax
+// against the wave's running reference, O^T += V^T P^T (V rows at `av`).
+template <int DP, bool HAS_BIAS, bool CAUSAL, int BN = 64>
 __device__ __forceinline__ void fwd32_tile(const Params& p, const F32Offsets<DP>& lo, uint32_t ak,
                                            uint32_t av, int k0, int cls,
                                            const f32x4 (&qf)[DP / 8], f32x16 (&oacc)[DP / 32],
                                            float& m_ref, float& l_i, int64_t brow,
                                            const uint8_t* mrow, int qrow, int qw0, int g) {
-  constexpr int BN = 64, NC = DP / 8, NDB = DP / 32;
+  constexpr int NKB = BN / 32, NA = 2 * NKB, NC = DP / 8, NDB = DP / 32;
   const uint32_t at = ak;
-    // S^T = K Q^T: two 32-key blocks, each over two halves of the head dim
-    // (four independent accumulators), fragments read a step ahead.
-    f32x16 sacc[4];
+    // S^T = K Q^T: each 32-key block over two halves of the head dim
+    // (independent accumulators, summed after), fragments read a step
+    // ahead.
+    f32x16 sacc[NA];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < NA; ++u)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[u][r] = 0.f;
     {
       constexpr int NH = NC / 2;
-      f32x4 a[2][4], bq[4];
+      f32x4 a[2][NA], bq[NA];
       auto rd = [&](f32x4* x, int c) NXA_INLINE {
-        x[0] = lo.row(at, 0, c);
-        x[1] = lo.row(at, 1, c);
-        x[2] = lo.row(at, 0, c + NH);
-        x[3] = lo.row(at, 1, c + NH);
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) x[kb] = lo.row(at, kb, c);
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) x[NKB + kb] = lo.row(at, kb, c + NH);
       };
       rd(a[0], 0);
 #pragma unroll
       for (int c = 0; c < NH; ++c) {
         if (c + 1 < NH) rd(a[(c + 1) & 1], c + 1);
-        bq[0] = bq[1] = qf[c];
-        bq[2] = bq[3] = qf[c + NH];
-        mma4n<4>(sacc, a[c & 1], bq);
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) bq[kb] = qf[c];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) bq[NKB + kb] = qf[c + NH];
+        mma4n<NA>(sacc, a[c & 1], bq);
       }
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * NA, 0);
 #pragma unroll
       for (int c = 0; c + 2 < NH; ++c) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 16, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4 * NA, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, NA, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 32, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8 * NA, 0);
     }
-    f32x16 sv[2];
+    f32x16 sv[NKB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sv[kb][r] = sacc[kb][r] + sacc[2 + kb][r];
+      for (int r = 0; r < 16; ++r) sv[kb][r] = sacc[kb][r] + sacc[NKB + kb][r];
 
     // Logits.  Fast path (no bias, nothing masked in the tile): the scale
     // is folded into the exponent's FMA and the max is taken on raw scores.
@@ -232,7 +235,7 @@ __device__ __forceinline__ void fwd32_tile(const Params& p, const F32Offsets<DP>
     if (general) {
       cc = 1.0f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int key0 = k0 + kb * 32 + 8 * c + 4 * g;
@@ -254,7 +257,7 @@ __device__ __forceinline__ void fwd32_tile(const Params& p, const F32Offsets<DP>
     }
     float mt = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sv[kb][r]);
     mt = fmaxf(mt, shfl_xor32(mt)) * cc;
@@ -271,7 +274,7 @@ __device__ __forceinline__ void fwd32_tile(const Params& p, const F32Offsets<DP>
     const float neg_m = (m_ref == -INFINITY) ? 0.f : -m_ref;
     float rs = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float e = fast_exp2(__builtin_fmaf(sv[kb][r], cc, neg_m));
@@ -280,29 +283,33 @@ __device__ __forceinline__ void fwd32_tile(const Params& p, const F32Offsets<DP>
       }
     l_i += rs;
 
-    // O^T += V^T P^T, the NDB accumulators interleaved, fragments read a
-    // step ahead.
+    // O^T += V^T P^T, the accumulators of NDH column blocks interleaved
+    // (all NDB, or at head dim 256 one half and then the other), fragments
+    // read a step ahead.
     {
-      f32x4 a[2][NDB], bb[NDB];
-      auto rd = [&](f32x4* x, int step) NXA_INLINE {
+      constexpr int NH = NDB > 4 ? 2 : 1, NDH = NDB / NH, NS = 4 * NKB, NU = NH * NS;
+      f32x4 a[2][NDH], bb[NDH];
+      auto rd = [&](f32x4* x, int u) NXA_INLINE {
+        const int step = u % NS, d0 = (u / NS) * NDH;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) x[db] = lo.tr(av, step >> 2, step & 3, db);
+        for (int k = 0; k < NDH; ++k) x[k] = lo.tr(av, step >> 2, step & 3, d0 + k);
       };
       rd(a[0], 0);
 #pragma unroll
-      for (int step = 0; step < 8; ++step) {
-        if (step + 1 < 8) rd(a[(step + 1) & 1], step + 1);
+      for (int u = 0; u < NU; ++u) {
+        if (u + 1 < NU) rd(a[(u + 1) & 1], u + 1);
+        const int step = u % NS;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) bb[db] = pack4(sv[step >> 2], step & 3);
-        mma4n<NDB>(oacc, a[step & 1], bb);
+        for (int k = 0; k < NDH; ++k) bb[k] = pack4(sv[step >> 2], step & 3);
+        mma4n<NDH>(oacc + (u / NS) * NDH, a[u & 1], bb);
       }
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8 * NDB, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8 * NDH, 0);
 #pragma unroll
-      for (int step = 0; step < 6; ++step) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4 * NDB, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4 * NDB, 0);
+      for (int u = 0; u + 2 < NU; ++u) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4 * NDH, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4 * NDH, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8 * NDB, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8 * NDH, 0);
     }
 
 }
@@ -318,10 +325,10 @@ __device__ __forceinline__ void fwd32_tile(const Params& p, const F32Offsets<DP>
 // ---------------------------------------------------------------------------
 template <int DP, bool HAS_BIAS, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void fwd32_kernel(const Params p) {
-  constexpr int BM = 128, BN = 64, NC = DP / 8, NDB = DP / 32;
+  constexpr int BM = 128, BN = DP > 128 ? 32 : 64, NC = DP / 8, NDB = DP / 32;
   constexpr int TILE = BN * DP * 4;
   constexpr int STAGE = 2 * TILE;  // K, V
-  using S = F32Stream<DP>;
+  using S = F32Stream<DP, 4, BN, (DP > 128)>;
   __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
   __shared__ uint32_t lst[kF32MaxTiles];
 
@@ -375,8 +382,8 @@ __global__ __launch_bounds__(256, 1) void fwd32_kernel(const Params p) {
   auto issue = [&](int i, int st) NXA_INLINE {
     const int t = i < n ? (int)(lst[i] & 0xffff) : nk;
     const uint32_t at = lds0 + st * STAGE;
-    const i32x4 rk = tile_rsrc(kp, p.k_str[2], t * BN, p.Lk, p.D);
-    const i32x4 rv = tile_rsrc(vp, p.v_str[2], t * BN, p.Lk, p.Dv);
+    const i32x4 rk = tile_rsrc<BN>(kp, p.k_str[2], t * BN, p.Lk, p.D);
+    const i32x4 rv = tile_rsrc<BN>(vp, p.v_str[2], t * BN, p.Lk, p.Dv);
 #pragma unroll
     for (int m = 0; m < S::CNT; ++m) {
       ks.issue(rk, at, m, wave);
@@ -394,8 +401,8 @@ __global__ __launch_bounds__(256, 1) void fwd32_kernel(const Params p) {
     const int k0 = t * BN;
     issue(i + 1, st ^ 1);
 
-    fwd32_tile<DP, HAS_BIAS, CAUSAL>(p, lo, at, at + TILE, k0, cls, qf, oacc, m_ref, l_i, brow,
-                                      mrow, qrow, qw0, g);
+    fwd32_tile<DP, HAS_BIAS, CAUSAL, BN>(p, lo, at, at + TILE, k0, cls, qf, oacc, m_ref, l_i,
+                                          brow, mrow, qrow, qw0, g);
 
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
@@ -1073,7 +1080,8 @@ __global__ __launch_bounds__(256, 1) void dq32_kernel(const Params p) {
 // Launchers: false when the problem is outside what these kernels take
 // (head dim above 128, or more tiles than a block lists).
 bool launch_fwd32(Params p, int dp, hipStream_t stream) {
-  if (dp > 128 || (p.Lk + 63) / 64 > kF32MaxTiles) return false;
+  const int bn = dp > 128 ? 32 : 64;
+  if (dp > 256 || (p.Lk + bn - 1) / bn > kF32MaxTiles) return false;
   p.nqt = (p.Lq + 127) / 128;
   // Fewer 128-query blocks than a quarter of the CUs, at head dim 64 and
   // with at least two key tiles: the key-split kernel, four blocks per
@@ -1100,6 +1108,14 @@ bool launch_fwd32(Params p, int dp, hipStream_t stream) {
     } else {
       if (p.causal) go(fwd32_kernel<64, false, true>);
       else go(fwd32_kernel<64, false, false>);
+    }
+  } else if (dp == 256) {
+    if (p.has_bias) {
+      if (p.causal) go(fwd32_kernel<256, true, true>);
+      else go(fwd32_kernel<256, true, false>);
+    } else {
+      if (p.causal) go(fwd32_kernel<256, false, true>);
+      else go(fwd32_kernel<256, false, false>);
     }
   } else {
     if (p.has_bias) {
