@@ -65,13 +65,13 @@ PEAK_HBM_GBS = 8000.0
 # TRAFFIC_SRC is the fingerprint (_src_fingerprint) of the attention kernel
 # sources the passes ran; when the sources differ, the figure describes other
 # kernels and is reported as stale (traffic null, the old figure beside it).
-TRAFFIC_SRC = '6777300c44b6c5ef'
+TRAFFIC_SRC = 'c3c2462c1eba4563'
 MEASURED_TRAFFIC = {
-    'c1': ('fwd', 6113970),
-    'c2': ('dkdv', 910301884),
-    'c3': ('dkdv', 1619900596),
-    'c4': ('fwd', 4431188824),
-    'c5': ('dkdv', 706605480),
+    'c1': ('fwd', 6102723),
+    'c2': ('dkdv', 910496004),
+    'c3': ('dkdv', 1619672291),
+    'c4': ('fwd', 4431237660),
+    'c5': ('dkdv', 706765667),
 }
 # VALU instructions (wave64) of the selective scan's backward pass (all five
 # kernels) per step at the ssm configuration, transcendental instructions
