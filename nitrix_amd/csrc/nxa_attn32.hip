@@ -1,5 +1,5 @@
-// fp32 attention kernels (forward, dK / dV and dQ) at padded head dims 64
-// and 128.
+// fp32 attention kernels (forward, dK / dV and dQ) at padded head dims 64,
+// 128 and 256.
 //
 // Same math as the 16-bit kernels and the reference's Pallas kernels
 // (src/nitrix/_kernels/cuda/attention.py:85-156 forward, :272-332 dK/dV,
@@ -13,8 +13,9 @@
 // the matrix core, not by LDS or VALU issue: a block of 4 waves (one per
 // SIMD, up to 512 registers each) holds its 128 queries (forward, dQ) or
 // keys (dK/dV) stationary and streams the other side's [64 x DP] fp32 tiles
-// through a double-buffered LDS ring, filled by direct global -> LDS copies
-// one tile ahead while the current one is consumed.  No transposed copies
+// ([32 x DP] at head dim 256) through a double-buffered LDS ring, filled by
+// direct global -> LDS copies one tile ahead while the current one is
+// consumed.  No transposed copies
 // are made: the products that contract over the streamed rows (O^T = V^T
 // P^T, dV^T = dO^T P, dK^T = Q^T dS, dQ^T = K^T dS^T) read their A operand
 // as four ds_read_b32 per fragment from the row-major tile -- bandwidth the
@@ -315,7 +316,8 @@ __device__ __forceinline__ void fwd32_tile(const Params& p, const F32Offsets<DP>
 }
 
 // ---------------------------------------------------------------------------
-// Forward.  Block = 4 waves x 32 queries; key tiles of 64 rows.  A wave holds
+// Forward.  Block = 4 waves x 32 queries; key tiles of 64 rows (32 at head
+// dim 256, so that two stages of K and V fit the LDS).  A wave holds
 // its queries' Q stationary and forms S^T = K Q^T with the query on the
 // lane's column, so the row max and sum take one lane ^ 32 exchange and P^T
 // feeds O^T += V^T P^T from registers.  The running max is raised only when
@@ -1078,7 +1080,7 @@ __global__ __launch_bounds__(256, 1) void dq32_kernel(const Params p) {
 }
 
 // Launchers: false when the problem is outside what these kernels take
-// (head dim above 128, or more tiles than a block lists).
+// (more streamed tiles than a block lists).
 bool launch_fwd32(Params p, int dp, hipStream_t stream) {
   const int bn = dp > 128 ? 32 : 64;
   if (dp > 256 || (p.Lk + bn - 1) / bn > kF32MaxTiles) return false;
