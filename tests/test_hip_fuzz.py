@@ -8,6 +8,18 @@ gradient (dbias included) against the float64 oracle at the dtype's budget,
 through the same C ABI as the fixed cases of ``test_hip_parity.py``.  The
 point is combinations the fixed cases do not list; the draws are fixed by
 the seeds, so a failure names a reproducible case.
+
+The gradients are checked against the oracle's backward fed the stored
+forward output, from which the reference's fused backward forms
+delta = rowsum(o * do) (``attention.py:600-622``), with the budget
+``tol * max|ref| + u * M``: M bounds the terms whose difference forms dS
+(``M = max scale * sum_j P_ij (sum|dO_i||v_j| + sum|o_i||dO_i|) |k_j|`` for
+dQ, likewise for dK and dS itself for dbias) and u is the rounding of the
+kernels' fp32 intermediates (2^-24; 2^-16 for the 16-bit kernels, whose
+-delta enters the dP products as a two-term bf16 split).  The term only
+matters where dS cancels almost entirely: an explicit scale that makes the
+softmax one-hot, or a single key (the exact gradient of q, k and the bias
+is then zero).
 """
 
 from __future__ import annotations
@@ -53,7 +65,20 @@ def _bias_shape(kind, B, H, s, t):
             'query': (B, H, 1, t), 'shared': (s, t), 'head': (B, 1, s, t)}[kind]
 
 
-@pytest.mark.parametrize('seed', range(48))
+def _cancel_bounds(q, k, v, g, o, bias, mask, scale, causal, bias_shape):
+    """M for dQ, dK and dbias (float64): the magnitudes of the terms that
+    cancel in dS = P (dP - delta)."""
+    logits, qa, ka = O._logits(q, k, bias, mask, scale, causal, False, np.dtype(np.float64))
+    p = O._softmax(logits)
+    ag, av, ao = np.abs(g.astype(np.float64)), np.abs(v.astype(np.float64)), np.abs(o)
+    w = p * (np.matmul(ag, np.swapaxes(av, -1, -2)) + np.sum(ao * ag, axis=-1, keepdims=True))
+    m_dq = scale * np.max(np.matmul(w, np.abs(ka)))
+    m_dk = scale * np.max(np.matmul(np.swapaxes(w, -1, -2), np.abs(qa)))
+    m_db = 0.0 if bias_shape is None else float(np.max(O.unbroadcast(w, bias_shape)))
+    return {'dq': m_dq, 'dk': m_dk, 'dv': 0.0, 'dbias': m_db}
+
+
+@pytest.mark.parametrize('seed', range(416))
 def test_random_configuration(seed):
     c = _case(seed)
     dtype, d, dv, B, H, s, t = (c[k] for k in ('dtype', 'd', 'dv', 'B', 'H', 's', 't'))
@@ -92,14 +117,18 @@ def test_random_configuration(seed):
         return  # gradients through NaN rows are NaN by definition
     out.backward(_to(g, dtype))
     torch.cuda.synchronize()
+    o = got.astype(np.float64)
     dq, dk, dvr, db = O.sdpa_backward(q, k, v, g, bias=bias, mask=mask, scale=scale,
-                                      causal=c['causal'], acc_dtype=np.float64)
+                                      causal=c['causal'], acc_dtype=np.float64, out=o)
+    u = 2.0 ** -24 if dtype == torch.float32 else 2.0 ** -16
+    bound = _cancel_bounds(q, k, v, g, o, bias, mask, scale, c['causal'], bshape)
     checks = [('dq', tq.grad, dq), ('dk', tk.grad, dk), ('dv', tv.grad, dvr)]
     if bias is not None:
         checks.append(('dbias', tb.grad, db))
     for name, got_t, want in checks:
         a = got_t.float().cpu().numpy()
         assert a.shape == want.shape, (name, a.shape, want.shape)
-        e = relerr(a, want)
-        print(f'  {name} relerr {e:.2e}', flush=True)
-        assert e <= tol, f'{name} relerr {e:.3e}'
+        err = float(np.max(np.abs(a - want))) if a.size else 0.0
+        budget = tol * float(np.max(np.abs(want))) + u * bound[name] if a.size else 0.0
+        print(f'  {name} relerr {relerr(a, want):.2e} err {err:.2e} budget {budget:.2e}', flush=True)
+        assert err <= budget, f'{name} error {err:.3e} > budget {budget:.3e}'

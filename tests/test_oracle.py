@@ -267,6 +267,31 @@ def test_backward_fd_value_head_dim_differs(dv):
     _fd_check(lambda s, t: (2, 2, s, t), causal=True, with_mask=True, dv=dv)
 
 
+def test_backward_delta_from_a_stored_output():
+    """``out=``: delta taken from a given forward output, as the reference's
+    backward takes it from its stored residual (``attention.py:600-622``).
+    Given the exact output it reproduces the default; given a perturbed one
+    (O + E), every row of dS sums to delta_exact - delta_out =
+    -rowsum(E * dO) (the rows of P sum to one, and sum_j P dP = delta_exact),
+    which a full bias returns as dbias; dV does not depend on it."""
+    rng = np.random.RandomState(5)
+    b, h, s, t, d, dv = 2, 2, 5, 7, 4, 3
+    q, k = rng.standard_normal((b, h, s, d)), rng.standard_normal((b, h, t, d))
+    v, g = rng.standard_normal((b, h, t, dv)), rng.standard_normal((b, h, s, dv))
+    bias = rng.standard_normal((b, h, s, t))
+    kw = dict(bias=bias, scale=0.6, acc_dtype=np.float64)
+    exact = O.sdpa_forward(q, k, v, **kw)
+    ref = O.sdpa_backward(q, k, v, g, **kw)
+    same = O.sdpa_backward(q, k, v, g, out=exact, **kw)
+    for x, y in zip(ref, same):
+        np.testing.assert_allclose(y, x, rtol=1e-12, atol=1e-12)
+    e = 1e-3 * rng.standard_normal(exact.shape)
+    pert = O.sdpa_backward(q, k, v, g, out=exact + e, **kw)
+    np.testing.assert_allclose(pert[3].sum(-1), -(e * g).sum(-1), rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(pert[2], ref[2], rtol=1e-12, atol=1e-12)
+    assert np.abs(pert[0] - ref[0]).max() > 1e-6  # dq does move with delta
+
+
 def test_qk_rms_norm_vjp_matches_finite_differences():
     rng = np.random.RandomState(5)
     z = rng.standard_normal((3, 2, 7))
