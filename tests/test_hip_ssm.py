@@ -264,7 +264,7 @@ def test_inference_forward_matches_training_forward():
     assert np.array_equal(y0, y1)
 
 
-@pytest.mark.parametrize('seed', range(6))
+@pytest.mark.parametrize('seed', range(64))
 def test_random_shapes(seed):
     rng = np.random.RandomState(100 + seed)
     lead = tuple(int(v) for v in rng.randint(1, 3, size=rng.randint(0, 3)))
