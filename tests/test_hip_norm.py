@@ -257,3 +257,66 @@ def test_qk_norm_outside_the_fused_backward_uses_the_norm_passes():
         for nm, got, want in (('dq', tq.grad, dq), ('dk', tk.grad, dk), ('dv', tv.grad, dvr)):
             e = relerr(got.float().cpu().numpy(), want)
             assert e <= tol, (dtype, nm, e)
+
+
+@pytest.mark.parametrize('seed', range(64))
+def test_fused_qk_norm_random_configuration(seed):
+    """Seeded random problems on the fused qk-norm path (bf16 / fp16): head
+    dims 8-256 with d_v != d in about a third, ragged lengths, key padding
+    or random masks, full or query-broadcast biases, causal; out at the
+    dtype's attention budget, every gradient against the float64 chain
+    (normalise, round, attention, attention VJP with delta from the stored
+    output as the reference's backward forms it, norm VJP)."""
+    from nitrix_amd import scaled_dot_product_attention
+
+    rng = np.random.default_rng(5000 + seed)
+    name = ('bf16', 'f16')[seed % 2]
+    dtype, rnd = DT[name], ROUND[name]
+    tol = 2e-2 if name == 'bf16' else 2e-3
+    d = int(rng.choice([8, 40, 64, 72, 96, 128, 136, 192, 256]))
+    dv = d if rng.random() < 0.7 else int(rng.choice([8, 32, 64, 128, 256]))
+    B, H = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+    s, t = int(rng.integers(2, 260)), int(rng.integers(2, 300))
+    causal = bool(rng.random() < 0.3)
+    mk = str(rng.choice(['none', 'keypad', 'random']))
+    bk = str(rng.choice(['none', 'full', 'row']))
+    q = rnd(rng.standard_normal((B, H, s, d)).astype(np.float32) * 3)
+    k = rnd(rng.standard_normal((B, H, t, d)).astype(np.float32) * 3)
+    v = rnd(rng.standard_normal((B, H, t, dv)).astype(np.float32))
+    g = rnd(rng.standard_normal((B, H, s, dv)).astype(np.float32))
+    bshape = {'none': None, 'full': (B, H, s, t), 'row': (B, H, 1, t)}[bk]
+    bias = None if bshape is None else rnd(rng.standard_normal(bshape).astype(np.float32))
+    mask = None
+    if mk == 'keypad':
+        valid = rng.integers(1, t + 1, size=B)
+        mask = (np.arange(t)[None, :] < valid[:, None])[:, None, None, :]
+    elif mk == 'random':
+        mask = rng.random((B, H, s, t)) < 0.5
+        mask[..., 0] = True
+    print(f'[case] qk-norm seed {seed}: {name} B{B} H{H} s{s} t{t} d{d} dv{dv} '
+          f'causal={causal} mask={mk} bias={bk}', flush=True)
+    to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(_dev(), dtype).requires_grad_(True)  # noqa: E731
+    tq, tk, tv = to(q), to(k), to(v)
+    tb = None if bias is None else to(bias)
+    tm = None if mask is None else torch.from_numpy(np.ascontiguousarray(mask)).to(_dev())
+    out = scaled_dot_product_attention(tq, tk, tv, bias=tb, mask=tm, causal=causal,
+                                       qk_norm=True, backend='hip')
+    out.backward(torch.from_numpy(g).to(_dev(), dtype))
+    torch.cuda.synchronize()
+    qh, kh = rnd(O.qk_rms_norm(q)), rnd(O.qk_rms_norm(k))
+    ref = O.sdpa_forward(qh, kh, v, bias=bias, mask=mask, causal=causal, acc_dtype=np.float64)
+    o = out.detach().float().cpu().numpy().astype(np.float64)
+    e = relerr(o, ref)
+    print(f'  out relerr {e:.2e}', flush=True)
+    assert e <= tol, ('out', e)
+    dqh, dkh, dvr, dbr = O.sdpa_backward(qh, kh, v, g, bias=bias, mask=mask, causal=causal,
+                                         acc_dtype=np.float64, out=o)
+    checks = [('dq', tq.grad, O.qk_rms_norm_vjp(q.astype(np.float64), dqh)),
+              ('dk', tk.grad, O.qk_rms_norm_vjp(k.astype(np.float64), dkh)),
+              ('dv', tv.grad, dvr)]
+    if bias is not None:
+        checks.append(('dbias', tb.grad, dbr))
+    for nm, got, want in checks:
+        e = relerr(got.float().cpu().numpy(), want)
+        print(f'  {nm} relerr {e:.2e}', flush=True)
+        assert e <= tol, (nm, e)
