@@ -15,8 +15,8 @@ delta = rowsum(o * do) (``attention.py:600-622``), with the budget
 ``tol * max|ref| + u * M``: M bounds the terms whose difference forms dS
 (``M = max scale * sum_j P_ij (sum|dO_i||v_j| + sum|o_i||dO_i|) |k_j|`` for
 dQ, likewise for dK and dS itself for dbias) and u is the rounding of the
-kernels' fp32 intermediates (2^-24; 2^-16 for the 16-bit kernels, whose
--delta enters the dP products as a two-term bf16 split).  The term only
+kernels' fp32 intermediates (2^-24; 2^-16 for the 16-bit kernels, whose dQ
+kernel adds -delta to its dP products as a two-term bf16 split).  The term only
 matters where dS cancels almost entirely: an explicit scale that makes the
 softmax one-hot, or a single key (the exact gradient of q, k and the bias
 is then zero).
