@@ -758,14 +758,59 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
   auto infos_uni = [&](const Infos& r) NXA_INLINE -> Infos {
     return {uni(r.kv), uni(r.bias), uni(r.sm)};
   };
-  // Matrix work of tile i: O += P(i-1) V(i-1), then S = K(i) Q^T.
-  auto mfma_phase = [&](int i) NXA_INLINE {
+  // Matrix work of tile i: O += P(i-1) V(i-1), then S = K(i) Q^T, with
+  // `between` after each S product.
+  auto mfma_phase = [&](int i, auto&& between) NXA_INLINE {
     // The wave feeding the matrix core issues first whenever it can; the
     // softmax wave of the pair fills the remaining issue slots.
     __builtin_amdgcn_s_setprio(FWD_PRIO);
     if (i > 0) pv(i - 1);
-    if (i < n) qk(i, [](int) {});
+    if (i < n) qk(i, between);
     __builtin_amdgcn_s_setprio(0);
+  };
+  auto no_copy = [](int) {};
+  // The wave's K / V copies of tile i + AHEAD spread over the S products of
+  // tile i, one every SPC products (the row bias copy goes first), instead
+  // of holding the wave at the copy path before its first product: `body`
+  // receives the callback that qk runs after each product.
+  auto with_copies = [&](auto lt, int i, const Infos& f, auto&& body) NXA_INLINE {
+    const bool nx = i + AHEAD < n;
+    const int k0n = nx ? tile_at(lt, i + AHEAD, f.kv) * BN : 0;
+    const uint32_t atn = lds0 + ((i + AHEAD) % NST) * STAGE_BYTES;
+    if constexpr (BMODE == kFbRow) {
+      if (nx) {
+        const int kk = min(k0n + 2 * c32, p.Lk - 2);
+        dma4_sv(bp, 2u * (uint32_t)kk, atn + 2 * TILE_BYTES + wave * 256);
+      }
+    }
+    const T* kb = kp + (int64_t)k0n * ks;
+    const T* vb = vp + (int64_t)k0n * vs;
+    uint32_t ok[KS::CNT], ov[KS::CNT];
+#pragma unroll
+    for (int m = 0; m < KS::CNT; ++m) {
+      ok[m] = ksm.off[m];
+      ov[m] = vsm.off[m];
+    }
+    if (nx && k0n + BN > p.Lk) {
+      // Tail tile: rows past Lk read the last row.
+#pragma unroll
+      for (int m = 0; m < KS::CNT; ++m) {
+        const int r = min(KS::row_of(m, wave, lane), p.Lk - 1 - k0n);
+        ok[m] = 2u * (uint32_t)(r * ks + KS::col_of(m, wave, lane, p.D));
+        ov[m] = 2u * (uint32_t)(r * vs + KS::col_of(m, wave, lane, p.Dv));
+      }
+    }
+    constexpr int SPC = NC / KS::CNT;  // S products per copy (2 NC products, 2 CNT copies)
+    static_assert(NC % KS::CNT == 0, "copies spread evenly over the S products");
+    body([&](int j) NXA_INLINE {
+      if (nx && j % SPC == SPC - 1) {
+        const int c = j / SPC;
+        if (c < KS::CNT)
+          dma16_sv(kb, ok[c], atn + (c * NW + wave) * 1024);
+        else
+          dma16_sv(vb, ov[c - KS::CNT], atn + TILE_BYTES + ((c - KS::CNT) * NW + wave) * 1024);
+      }
+    });
   };
   // VALU work of tile i: element-wise pass (general tiles), P = exp(...)
   // and, when needed, the row max and a lazy reference update (O is
@@ -804,7 +849,11 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
     // stage of tile t-2 free for the copies issued after it); a second one
     // between the phases keeps the pairs in step only with full bias tiles,
     // whose HBM stream it paces (without bias tiles it costs 1-2.5 %).
+    // Without bias tiles each wave's copies of tile t+2 ride along with its
+    // own S products, which keeps the copy path from holding both waves of
+    // a SIMD after the barrier (tile t+2 has more than a tile to land).
     constexpr bool MID_BARRIER = BMODE == kFbTile;
+    constexpr bool COPY_IN_MFMA = BMODE != kFbTile && AHEAD >= 2;
     auto run = [&](auto lag_tag, auto lt) {
       constexpr bool LAG = decltype(lag_tag)::value;
       constexpr bool LIST = decltype(lt)::value;
@@ -816,20 +865,26 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
         if constexpr (LIST) r = infos_raw(i + 1, LAG ? i : i + 1);
         wait_tile(i);
         barrier_nofence();
-        issue_ahead(lt, i, f);
+        auto matrix = [&]() NXA_INLINE {
+          if constexpr (COPY_IN_MFMA)
+            with_copies(lt, i, f, [&](auto&& between) NXA_INLINE { mfma_phase(i, between); });
+          else
+            mfma_phase(i, no_copy);
+        };
+        if constexpr (!COPY_IN_MFMA) issue_ahead(lt, i, f);
         if (LAG) valu_phase(lt, i - 1, f.sm);
-        else mfma_phase(i);
+        else matrix();
         if constexpr (MID_BARRIER) barrier_nofence();
-        if (LAG) mfma_phase(i);
+        if (LAG) matrix();
         else valu_phase(lt, i, f.sm);
         if constexpr (LIST) f = infos_uni(r);
       }
       if (n > 0) {
         barrier_nofence();
         if (LAG) valu_phase(lt, n - 1, f.sm);
-        else mfma_phase(n);
+        else mfma_phase(n, no_copy);
         barrier_nofence();
-        if (LAG) mfma_phase(n);
+        if (LAG) mfma_phase(n, no_copy);
       }
     };
     if (wave >= NW / 2) {
@@ -855,44 +910,8 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 2) void fwd16_kernel(const 
         barrier_nofence();
         if constexpr (COPY_IN_S) {
           // The K / V copies of tile i + AHEAD ride along with the S
-          // products (one per two), instead of holding the wave at the copy
-          // path before its first product (the row bias copy goes first).
-          const bool nx = i + AHEAD < n;
-          const int k0n = nx ? tile_at(lt, i + AHEAD, f.kv) * BN : 0;
-          const uint32_t atn = lds0 + ((i + AHEAD) % NST) * STAGE_BYTES;
-          if constexpr (BMODE == kFbRow) {
-            if (nx) {
-              const int kk = min(k0n + 2 * c32, p.Lk - 2);
-              dma4_sv(bp, 2u * (uint32_t)kk, atn + 2 * TILE_BYTES + wave * 256);
-            }
-          }
-          const T* kb = kp + (int64_t)k0n * ks;
-          const T* vb = vp + (int64_t)k0n * vs;
-          uint32_t ok[KS::CNT], ov[KS::CNT];
-#pragma unroll
-          for (int m = 0; m < KS::CNT; ++m) {
-            ok[m] = ksm.off[m];
-            ov[m] = vsm.off[m];
-          }
-          if (nx && k0n + BN > p.Lk) {
-            // Tail tile: rows past Lk read the last row.
-#pragma unroll
-            for (int m = 0; m < KS::CNT; ++m) {
-              const int r = min(KS::row_of(m, wave, lane), p.Lk - 1 - k0n);
-              ok[m] = 2u * (uint32_t)(r * ks + KS::col_of(m, wave, lane, p.D));
-              ov[m] = 2u * (uint32_t)(r * vs + KS::col_of(m, wave, lane, p.Dv));
-            }
-          }
-          static_assert(2 * NC == 4 * KS::CNT, "one copy per two S products");
-          qk(i, [&](int j) NXA_INLINE {
-            if (nx && (j & 1)) {
-              const int c = j >> 1;
-              if (c < KS::CNT)
-                dma16_sv(kb, ok[c], atn + (c * NW + wave) * 1024);
-              else
-                dma16_sv(vb, ov[c - KS::CNT], atn + TILE_BYTES + ((c - KS::CNT) * NW + wave) * 1024);
-            }
-          });
+          // products (one per two).
+          with_copies(lt, i, f, [&](auto&& between) NXA_INLINE { qk(i, between); });
         } else {
           issue_ahead(lt, i, f);
           qk(i, [](int) {});
