@@ -65,13 +65,13 @@ PEAK_HBM_GBS = 8000.0
 # TRAFFIC_SRC is the fingerprint (_src_fingerprint) of the attention kernel
 # sources the passes ran; when the sources differ, the figure describes other
 # kernels and is reported as stale (traffic null, the old figure beside it).
-TRAFFIC_SRC = 'c53be6318d52d8da'
+TRAFFIC_SRC = 'ddcab986b473d600'
 MEASURED_TRAFFIC = {
-    'c1': ('fwd', 6102722),
-    'c2': ('dkdv', 910359292),
-    'c3': ('dkdv', 1619892718),
-    'c4': ('fwd', 4431231843),
-    'c5': ('dkdv', 706690064),
+    'c1': ('fwd', 6102552),
+    'c2': ('dkdv', 910049830),
+    'c3': ('dkdv', 1620318596),
+    'c4': ('fwd', 4431223352),
+    'c5': ('dkdv', 706534159),
 }
 # VALU instructions (wave64) of the selective scan's backward pass (all five
 # kernels) per step at the ssm configuration, transcendental instructions
