@@ -1127,6 +1127,10 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
   constexpr int STAGE_BYTES = 2 * TILE_BYTES + ROWB_BYTES;
   constexpr int NST = DP == 64 ? 3 : 2;                // K / V stages (two blocks per CU)
   constexpr int CPT = 2 * KS::CNT + (ROW_BIAS ? 1 : 0);  // copies per wave per tile
+  // At D = 128 (two stages, so the next tile must land within the tile)
+  // the copies ride with the first key block's products, one per two, for
+  // the most time in flight; elsewhere one per four over both blocks.
+  constexpr bool COPY_EARLY = DP == 128;
   __shared__ __attribute__((aligned(16))) char smem[NST * STAGE_BYTES];
   __shared__ uint32_t ainfo[kMaxBwdTiles];  // active key tiles, in order: index | class << 30
   __shared__ int nact_s;
@@ -1387,8 +1391,7 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
     for (int kb = 0; kb < 2; ++kb) {
       // S^T (+ row bias) and dP^T: product j is S chunk j / 2 (j even) or
       // dP chunk j / 2 (j odd); A fragments are read PD products ahead, and
-      // this wave's copies of tile i + NST - 1 ride along (one per four
-      // products).
+      // this wave's copies of tile i + NST - 1 ride along (COPY_EARLY).
       f32x16 s;
       f32x16 dp = MB::first(ones, bdlt);
       if constexpr (ROW_BIAS) {
@@ -1418,11 +1421,15 @@ __global__ __launch_bounds__(256, DP > 128 ? 1 : 2) void dq16_kernel(const Param
           M::run(s, abuf[j % PD], qf[m]);
         if (j + PD < NP) abuf[j % PD] = afrag(j + PD);
         const int pc = kb * NP + j;  // product count in this tile
-        if ((pc & 3) == 3 && (pc >> 2) < CPT) copy_next(pc >> 2);
+        if constexpr (COPY_EARLY) {
+          if ((pc & 1) == 1 && (pc >> 1) < CPT) copy_next(pc >> 1);
+        } else {
+          if ((pc & 3) == 3 && (pc >> 2) < CPT) copy_next(pc >> 2);
+        }
       }
       if (kb == 1) {
 #pragma unroll
-        for (int jc = NP / 2; jc < CPT; ++jc) copy_next(jc);
+        for (int jc = COPY_EARLY ? NP : NP / 2; jc < CPT; ++jc) copy_next(jc);
       }
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, PD, 0);
 #pragma unroll
