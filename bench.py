@@ -65,13 +65,13 @@ PEAK_HBM_GBS = 8000.0
 # TRAFFIC_SRC is the fingerprint (_src_fingerprint) of the attention kernel
 # sources the passes ran; when the sources differ, the figure describes other
 # kernels and is reported as stale (traffic null, the old figure beside it).
-TRAFFIC_SRC = 'ddcab986b473d600'
+TRAFFIC_SRC = '31b32cd5e083de76'
 MEASURED_TRAFFIC = {
-    'c1': ('fwd', 6102552),
-    'c2': ('dkdv', 910049830),
-    'c3': ('dkdv', 1620318596),
-    'c4': ('fwd', 4431223352),
-    'c5': ('dkdv', 706534159),
+    'c1': ('fwd', 6102721),
+    'c2': ('dkdv', 910444756),
+    'c3': ('dkdv', 1619918515),
+    'c4': ('fwd', 4431184901),
+    'c5': ('dkdv', 706542360),
 }
 # VALU instructions (wave64) of the selective scan's backward pass (all five
 # kernels) per step at the ssm configuration, transcendental instructions
