@@ -287,10 +287,23 @@ def _layout_ok(x: torch.Tensor, epc: int) -> bool:
     return all(s % epc == 0 for s in x.stride()[:-1])
 
 
+def _lead_shape(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> tuple:
+    """The broadcast leading axes of q, k, v (``torch.broadcast_shapes``,
+    whose tensor machinery costs more host time than a whole small launch,
+    only when they differ)."""
+    lq, lk, lv = tuple(q.shape[:-2]), tuple(k.shape[:-2]), tuple(v.shape[:-2])
+    if lq == lk == lv:
+        return lq
+    return tuple(torch.broadcast_shapes(lq, lk, lv))
+
+
 def _as_bhld(x: torch.Tensor, lead: Sequence[int], nb: int, epc: int) -> torch.Tensor:
     L, d = x.shape[-2], x.shape[-1]
     h = lead[-1]
-    y = x.expand(*lead, L, d).reshape(nb, h, L, d)
+    if x.ndim == 4 and x.shape[0] == nb and x.shape[1] == h:
+        y = x  # already [nb, h, L, d]
+    else:
+        y = x.expand(*lead, L, d).reshape(nb, h, L, d)
     if not _layout_ok(y, epc):
         y = y.contiguous()
     return y
@@ -300,7 +313,10 @@ def _as_bhst(
     x: torch.Tensor, lead: Sequence[int], nb: int, s: int, t: int
 ) -> torch.Tensor:
     h = lead[-1]
-    y = x.expand(*lead, s, t).reshape(nb, h, s, t)
+    if x.ndim == 4 and tuple(x.shape) == (nb, h, s, t):
+        y = x  # already [nb, h, s, t]
+    else:
+        y = x.expand(*lead, s, t).reshape(nb, h, s, t)
     if (y.stride(-1) != 1 and t != 1) or not _row_stride_ok(y.stride(-2), y.element_size()):
         y = y.contiguous()
     return y
@@ -326,7 +342,7 @@ class _Prepared:
     def __init__(self, q, k, v, bias, mask, scale, causal):
         *_, s, d = q.shape
         t = k.shape[-2]
-        lead = tuple(torch.broadcast_shapes(q.shape[:-2], k.shape[:-2], v.shape[:-2]))
+        lead = _lead_shape(q, k, v)
         self.lead = lead
         self.batch = lead[:-1]
         self.h = lead[-1]
@@ -606,7 +622,7 @@ def _norm_fusable(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
         return False
     if max(q.shape[-1], v.shape[-1]) > _MAX_HEAD_DIM or q.shape[-1] % 8 or v.shape[-1] % 8:
         return False
-    lead = tuple(torch.broadcast_shapes(q.shape[:-2], k.shape[:-2], v.shape[:-2]))
+    lead = _lead_shape(q, k, v)
     return tuple(q.shape[:-2]) == lead and tuple(k.shape[:-2]) == lead
 
 
