@@ -300,7 +300,7 @@ def _lead_shape(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> tuple:
 def _as_bhld(x: torch.Tensor, lead: Sequence[int], nb: int, epc: int) -> torch.Tensor:
     L, d = x.shape[-2], x.shape[-1]
     h = lead[-1]
-    if x.ndim == 4 and x.shape[0] == nb and x.shape[1] == h:
+    if len(lead) == 2 and tuple(x.shape[:-2]) == tuple(lead):
         y = x  # already [nb, h, L, d]
     else:
         y = x.expand(*lead, L, d).reshape(nb, h, L, d)
@@ -313,7 +313,7 @@ def _as_bhst(
     x: torch.Tensor, lead: Sequence[int], nb: int, s: int, t: int
 ) -> torch.Tensor:
     h = lead[-1]
-    if x.ndim == 4 and tuple(x.shape) == (nb, h, s, t):
+    if len(lead) == 2 and tuple(x.shape) == (*lead, s, t):
         y = x  # already [nb, h, s, t]
     else:
         y = x.expand(*lead, s, t).reshape(nb, h, s, t)

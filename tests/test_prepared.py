@@ -117,3 +117,14 @@ def test_fast_and_general_routes_fill_the_same_descriptor():
     for a, b in ((fast.q, slow.q), (fast.k, slow.k), (fast.v, slow.v),
                  (fast.bias, slow.bias)):
         assert _same_view(a, b)
+
+
+def test_a_bias_that_does_not_broadcast_still_raises():
+    # Leading axes (2, 3) of q, k, v; a bias with a flattened batch of 6
+    # has the [nb, h, s, t] shape of neither and must not be taken as one.
+    q = torch.randn(2, 3, 4, 8, 64)
+    k = torch.randn(2, 3, 4, 8, 64)
+    v = torch.randn(2, 3, 4, 8, 64)
+    bias = torch.randn(6, 4, 8, 8)
+    with pytest.raises(RuntimeError):
+        A._Prepared(q, k, v, bias, None, 0.125, False)
