@@ -123,10 +123,19 @@ def reproducible(enabled: bool = True) -> Iterator[None]:
 # --- hardware --------------------------------------------------------------------
 
 
+# Architecture test per device index: a device's properties do not change
+# within a process, and the lookup costs more host time than a small launch.
+_GFX950_BY_INDEX: dict = {}
+
+
 def device_is_gfx950(device: Any) -> bool:
     """True for a ROCm device whose architecture is gfx950 (MI355X)."""
     if getattr(device, 'type', None) != 'cuda':
         return False
+    index = getattr(device, 'index', None)
+    hit = _GFX950_BY_INDEX.get(index) if index is not None else None
+    if hit is not None:
+        return hit
     import torch
 
     if torch.version.hip is None:
@@ -135,7 +144,10 @@ def device_is_gfx950(device: Any) -> bool:
         arch = torch.cuda.get_device_properties(device).gcnArchName
     except Exception:  # pragma: no cover - no usable device
         return False
-    return str(arch).partition(':')[0] == 'gfx950'
+    ok = str(arch).partition(':')[0] == 'gfx950'
+    if index is not None:
+        _GFX950_BY_INDEX[index] = ok
+    return ok
 
 
 def auto_backend(device: Any) -> ResolvedBackend:
