@@ -644,6 +644,13 @@ def scaled_dot_product_attention_hip(
     """
     _check_tileable(q, k, v)
     _lib.lib()  # a missing library is an error here, not a fallback
+    if not (torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (q, k, v, bias))):
+        # Nothing to differentiate: the forward alone, without the autograd
+        # node (whose bookkeeping costs host time a small call notices).
+        prep = _Prepared(q, k, v, bias, mask, float(scale), bool(causal))
+        o, _, _ = _forward(prep)
+        return o.reshape(*prep.lead, prep.s, prep.dv)
     return _SdpaHip.apply(q, k, v, bias, mask, float(scale), bool(causal))
 
 
